@@ -1,0 +1,202 @@
+"""Benchmark of the fused INT8 convrot linear on one MI355X.
+
+Workload (one step = one pass of the hot path over one batch): the DiT fused QKV projection, M=32768 tokens,
+K=5120, N=15360, Hadamard group 256, low-rank rank 64, no bias, synthetic seeded data resident in HBM:
+x bf16 N(0,1) with 0.5% outlier channels x30, qweight int8 U{-127..127}, wscale fp32 U(1e-3, 1e-2), low-rank
+down/up bf16 N(0, 0.02). A step is the whole fused layer: rotate+quantize, low-rank down projection, INT8 GEMM with
+the fused epilogue.
+
+value = 2*M*N*K int8 ops per step / measured step time (TOPS). The roofline object is for the dominant kernel
+(the GEMM): its average duration comes from HIP events recorded around every GEMM launch on the launch stream inside
+the timed region. The CPU baseline times the PyTorch-CPU path of the reference layer on a bounded row sample of the
+same workload on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+M, K, N, GROUP, RANK = 32768, 5120, 15360, 256, 64
+PEAK_INT8_TOPS = 5033.2  # MI355X dense INT8 MFMA: 256 CUs x 2.4 GHz x 8192 ops/clk
+PEAK_HBM_GBS = 8000.0
+METRIC = "convrot INT8 linear TOPS + % of MI355X INT8 MFMA peak, M=32768 K=5120"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_int8_gemm_qkv_m32768.txt")
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-rows", type=int, default=1024, help="row sample for the CPU baseline")
+    return p.parse_args()
+
+
+def make_inputs(torch, dev, seed=0):
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(M, K, device=dev, generator=gen)
+    cols = torch.randperm(K, device=dev, generator=gen)[: -(-K * 5 // 1000)]
+    x[:, cols] *= 30.0
+    x = x.to(torch.bfloat16)
+    qweight = torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8, generator=gen)
+    wscale = torch.rand(N, device=dev, generator=gen) * 9e-3 + 1e-3
+    down = (torch.randn(RANK, K, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    up = (torch.randn(N, RANK, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    return x, qweight, wscale, down, up
+
+
+def read_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, scaled by the
+    copy-kernel calibration), or None when no summary is committed."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(torch, rows, seed=0):
+    """The reference's CPU PyTorch path (int8.py:173-179, restated in oracle/torch_path.py) plus the low-rank
+    composition, on a `rows`-row sample of the workload: 1 warm-up then the median of 3 timed calls."""
+    from oracle import torch_path
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(seed)
+    x = (torch.randn(rows, K, generator=gen)).to(torch.bfloat16)
+    qweight = torch.randint(-127, 128, (N, K), dtype=torch.int8, generator=gen)
+    wscale = torch.rand(N, generator=gen) * 9e-3 + 1e-3
+    down = (torch.randn(RANK, K, generator=gen) * 0.02).to(torch.bfloat16)
+    up = (torch.randn(N, RANK, generator=gen) * 0.02).to(torch.bfloat16)
+    times = []
+    for i in range(4):
+        t0 = time.perf_counter()
+        torch_path.forward_torch(x, qweight, wscale, GROUP, down, up)
+        t = time.perf_counter() - t0
+        if i:
+            times.append(t)
+    t = statistics.median(times)
+    return {
+        "value": round(2.0 * rows * N * K / t / 1e12, 4),
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{rows} of {M} rows (K={K}, N={N}, G={GROUP}, rank {RANK}); median of 3 after 1 warm-up, "
+                  f"{t:.2f} s per call; torch {torch.__version__} CPU, {platform.processor() or platform.machine()}",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every run here has one MI355X; "
+              "the linear shards by rows with no communication, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from hyperflow_h3_flash_amd import Int8RotLinear
+    from hyperflow_h3_flash_amd.int8 import _kernels
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    x, qweight, wscale, down, up = make_inputs(torch, dev)
+    layer = Int8RotLinear(K, N, GROUP, rank=RANK).to(dev)
+    with torch.no_grad():
+        layer.qweight.copy_(qweight)
+        layer.wscale.copy_(wscale)
+        layer.down.weight.copy_(down)
+        layer.up.weight.copy_(up)
+    del qweight, wscale
+    kernels = _kernels()
+    stream = torch.cuda.current_stream(dev)
+
+    # per-kernel events: recorded around each launch on the launch stream (torch's current stream)
+    ev = {name: [] for name in ("rotate", "lowrank", "gemm")}
+
+    def step(record):
+        with torch.no_grad():
+            if record:
+                e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+                e[0].record(stream)
+            xq, sx = kernels.rotate_quant(x, GROUP)
+            if record:
+                e[1].record(stream)
+            u = kernels.lowrank_down(x, layer.down.weight)
+            if record:
+                e[2].record(stream)
+            y = kernels.int8_matmul(xq, layer.qweight, sx, layer.wscale, u=u, up=layer.up.weight)
+            if record:
+                e[3].record(stream)
+                ev["rotate"].append((e[0], e[1]))
+                ev["lowrank"].append((e[1], e[2]))
+                ev["gemm"].append((e[2], e[3]))
+        return y
+
+    # the timed step is exactly what Int8RotLinear.forward launches for a bf16 [M, K] input
+    with torch.no_grad():
+        torch.testing.assert_close(step(False), layer(x), rtol=0, atol=0)
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    ops = 2.0 * M * N * K
+    ms_per_step = elapsed / args.steps * 1e3
+    tops = ops * args.steps / elapsed / 1e12
+    avg_us = {k: statistics.mean(a.elapsed_time(b) for a, b in v) * 1e3 for k, v in ev.items()}
+    gemm_tops = ops / (avg_us["gemm"] * 1e-6) / 1e12
+    rotate_bytes = 2 * M * K + M * K + 4 * M
+    result = {
+        "metric": METRIC,
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded, config-2 distributions, resident in HBM)",
+        "config": {"workload": "DiT fused QKV convrot linear: rotate+quant, low-rank down, INT8 GEMM + fused "
+                               "epilogue", "M": M, "K": K, "N": N, "group": GROUP, "rank": RANK, "bias": False},
+        "pct_of_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
+        "kernel_us": {k: round(v, 2) for k, v in avg_us.items()},
+        "rotate_quant_GBs": round(rotate_bytes / (avg_us["rotate"] * 1e-6) / 1e9, 1),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(gemm_tops, 2),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+            "traffic": read_traffic(),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        del x, layer
+        torch.cuda.empty_cache()
+        result["cpu_baseline"] = cpu_baseline(torch, args.cpu_rows)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,28 @@
+"""MI355X-native INT8 "convrot" linear for HyperFlow H3 Flash: a drop-in for ``hyperflow_h3_flash.int8``.
+
+Importing the package does not touch the GPU or load the HIP library; the first device forward does.
+"""
+
+from .int8 import (
+    INT8_GEMMS,
+    KERNEL_OPTIONS,
+    ROTATE_QUANTS,
+    Int8RotLinear,
+    hadamard_factors,
+    regular_hadamard,
+    resolve_int8_gemm,
+    set_kernel_options,
+)
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "INT8_GEMMS",
+    "KERNEL_OPTIONS",
+    "ROTATE_QUANTS",
+    "Int8RotLinear",
+    "hadamard_factors",
+    "regular_hadamard",
+    "resolve_int8_gemm",
+    "set_kernel_options",
+]

@@ -1,0 +1,96 @@
+"""ctypes binding of ``libhf_convrot.so`` (the C ABI of include/hf_convrot.h) and the build recipe that makes it.
+
+The library is built in-tree by ``build_library()`` (hipcc, gfx950) and loaded from next to this file. There is no
+fallback: when the library is missing or does not load, ``library()`` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from functools import lru_cache
+
+PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PACKAGE_DIR)
+LIB_PATH = os.path.join(PACKAGE_DIR, "libhf_convrot.so")
+SOURCE = os.path.join(PACKAGE_DIR, "csrc", "convrot_abi.hip")
+ARCH = "gfx950"
+
+#: hipcc flags: CDNA4 only; fp-contract off keeps every multiply and add separately rounded as written; packed
+#: fp32 instructions are disabled.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+HF_OK = 0
+STATUS_NAMES = {
+    -1: "HF_ERR_ARGUMENT",
+    -2: "HF_ERR_GROUP",
+    -3: "HF_ERR_ALIGNMENT",
+    -4: "HF_ERR_LAUNCH",
+    -5: "HF_ERR_SIZE",
+}
+
+#: Every function include/hf_convrot.h declares, with its ctypes signature.
+_P, _I64, _I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+SIGNATURES = {
+    "hf_version": ([], ctypes.c_char_p),
+    "hf_strerror": ([ctypes.c_int], ctypes.c_char_p),
+    "hf_rotate_quant": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I32, _P], ctypes.c_int),
+    "hf_lowrank_down": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I32, _P], ctypes.c_int),
+    "hf_int8_linear": ([_P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
+                       ctypes.c_int),
+    "hf_int8_gemm_i32": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P], ctypes.c_int),
+    "hf_convrot_linear": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _P, _P, _P, _I64, _I64,
+                           _I64, _I64, _P], ctypes.c_int),
+}
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    path = os.path.join(rocm, "bin", "hipcc")
+    return path if os.path.exists(path) else "hipcc"
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile csrc/ into libhf_convrot.so for gfx950 (always recompiles). Returns the library path."""
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, SOURCE]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
+    if verbose and proc.stderr:
+        print(proc.stderr[-2000:])
+    os.replace(tmp, LIB_PATH)
+    library.cache_clear()
+    return LIB_PATH
+
+
+@lru_cache(maxsize=None)
+def library() -> ctypes.CDLL:
+    """The loaded library with argument types set. Raises RuntimeError when it is missing or does not load."""
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+            "(hipcc --offload-arch=gfx950)"
+        )
+    try:
+        lib = ctypes.CDLL(LIB_PATH)
+    except OSError as exc:
+        raise RuntimeError(f"cannot load {LIB_PATH}: {exc}") from exc
+    for name, (argtypes, restype) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    return lib
+
+
+def status_text(status: int) -> str:
+    return f"{STATUS_NAMES.get(status, status)}: {library().hf_strerror(status).decode()}"

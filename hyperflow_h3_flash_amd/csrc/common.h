@@ -1,0 +1,58 @@
+// Shared device helpers for the convrot kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hf {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+#define HF_LDS __attribute__((address_space(3)))
+
+// bf16 bit pattern -> fp32 (exact).
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet (torch's `.to(torch.bfloat16)`).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return ((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : r;
+}
+
+// Rounds an fp64 value to 8 significant bits (bf16 precision) with round-to-nearest-even, once, directly from the
+// fp64 bits: the kept bits end at bit 13 of the high word; bit 12 is the rounding bit and bits 11..0 of the high
+// word plus the whole low word are sticky. Adding 0xFFF + (lsb | sticky_low) carries into bit 13 exactly when RNE
+// rounds up. The result has at most 8 significant bits, so the fp32 conversion is exact (inf beyond fp32 range).
+__device__ __forceinline__ float round_f64_to_bf16_value(double t) {
+  unsigned long long u = __double_as_longlong(t);
+  uint32_t hi = (uint32_t)(u >> 32), lo = (uint32_t)u;
+  uint32_t c = ((hi >> 13) & 1u) | (lo != 0u ? 1u : 0u);
+  hi = (hi + 0x0fffu + c) & ~0x1fffu;
+  return (float)__longlong_as_double((long long)((unsigned long long)hi << 32));
+}
+
+// Wave-level exchange through LDS: make this wave's LDS writes visible to its own later reads, without a
+// workgroup barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Buffer resource for raw (stride 0) buffer loads: offsets at or beyond `bytes` read as zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+}  // namespace hf

@@ -1,0 +1,188 @@
+// Host launchers behind the C ABI declared in include/hf_convrot.h. One translation unit: the kernel sources are
+// included so a single hipcc invocation builds the shared library.
+#include <mutex>
+
+#include "../../include/hf_convrot.h"
+#include "int8_gemm.hip"
+#include "lowrank.hip"
+#include "rotate_quant.hip"
+
+namespace {
+
+constexpr int kMaxLds = 160 * 1024;
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+inline int launch_status() { return hipGetLastError() == hipSuccess ? HF_OK : HF_ERR_LAUNCH; }
+
+int log4_of(int32_t group) {
+  switch (group) {
+    case 4: return 1;
+    case 16: return 2;
+    case 64: return 3;
+    case 256: return 4;
+    default: return -1;
+  }
+}
+
+// Kernels that use more than 64 KiB of dynamic LDS must say so once per process.
+void allow_large_lds() {
+  static std::once_flag once;
+  std::call_once(once, [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<false>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<true>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<1>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<2>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<3>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<4>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipGetLastError();
+  });
+}
+
+int check_gemm_operands(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, int64_t M, int64_t N,
+                        int64_t K) {
+  if (!q || !w || M < 0 || N < 0 || K <= 0 || ldq < K || ldw < K) return HF_ERR_ARGUMENT;
+  if ((K % 16) || !aligned(q, 16) || !aligned(w, 16) || (ldq % 16) || (ldw % 16)) return HF_ERR_ALIGNMENT;
+  if (256 * ldq >= (int64_t(1) << 31) || 256 * ldw >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  if (M >= (int64_t(1) << 31) || N >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  return HF_OK;
+}
+
+int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream) {
+  allow_large_lds();
+  a.tiles_m = (a.M + hf::GBM - 1) / hf::GBM;
+  a.tiles_n = (a.N + hf::GBN - 1) / hf::GBN;
+  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+  if (tiles == 0) return HF_OK;
+  if (tiles >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  if (i32) {
+    hipLaunchKernelGGL(hf::int8_gemm_kernel<true>, dim3((unsigned)tiles), dim3(256), hf::kGemmLds, stream, a);
+  } else {
+    hipLaunchKernelGGL(hf::int8_gemm_kernel<false>, dim3((unsigned)tiles), dim3(256), hf::kGemmLds, stream, a);
+  }
+  return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* hf_version(void) { return "hf_convrot 0.1.0 gfx950"; }
+
+const char* hf_strerror(int status) {
+  switch (status) {
+    case HF_OK: return "ok";
+    case HF_ERR_ARGUMENT: return "invalid argument (null pointer, negative size or stride smaller than the row)";
+    case HF_ERR_GROUP: return "unsupported Hadamard group (4, 16, 64 or 256, dividing K)";
+    case HF_ERR_ALIGNMENT: return "pointer or stride breaks the 16-byte alignment rules";
+    case HF_ERR_LAUNCH: return "HIP kernel launch failed";
+    case HF_ERR_SIZE: return "size exceeds the kernels' index range";
+    default: return "unknown status";
+  }
+}
+
+int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int64_t K,
+                    int32_t group, hf_stream_t stream) {
+  if (M < 0 || K <= 0 || ldx < K || ldq < K) return HF_ERR_ARGUMENT;
+  if (M == 0) return HF_OK;
+  if (!x || !q || !sx) return HF_ERR_ARGUMENT;
+  const int lg = log4_of(group);
+  if (lg < 0 || K % group) return HF_ERR_GROUP;
+  if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16)) return HF_ERR_ALIGNMENT;
+  int waves = 4;
+  while (waves > 0 && hf::rotate_quant_lds_bytes(waves, (int)std::min<int64_t>(K, 1 << 30)) > (size_t)kMaxLds)
+    waves >>= 1;
+  if (waves == 0 || K > 77312) return HF_ERR_SIZE;
+  allow_large_lds();
+  const size_t lds = hf::rotate_quant_lds_bytes(waves, (int)K);
+  const int64_t blocks64 = (M + waves - 1) / waves;
+  const unsigned blocks = (unsigned)std::min<int64_t>(blocks64, int64_t(1) << 30);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (lg) {
+    case 1: hipLaunchKernelGGL(hf::rotate_quant_kernel<1>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    case 2: hipLaunchKernelGGL(hf::rotate_quant_kernel<2>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    case 3: hipLaunchKernelGGL(hf::rotate_quant_kernel<3>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    default: hipLaunchKernelGGL(hf::rotate_quant_kernel<4>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+  }
+  return launch_status();
+}
+
+int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_t ld_down, uint16_t* u,
+                    int64_t ldu, int64_t M, int64_t K, int32_t r, hf_stream_t stream) {
+  if (M < 0 || K <= 0 || r < 0 || ldx < K || ld_down < K || ldu < r) return HF_ERR_ARGUMENT;
+  if (M == 0 || r == 0) return HF_OK;
+  if (!x || !down || !u) return HF_ERR_ARGUMENT;
+  if (K % 16 || !aligned(x, 16) || !aligned(down, 16) || (ldx % 8) || (ld_down % 8) || !aligned(u, 8))
+    return HF_ERR_ALIGNMENT;
+  if (M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned blocks = (unsigned)((M + 31) / 32);
+  for (int32_t j0 = 0; j0 < r; j0 += 128) {
+    const int rr = std::min<int32_t>(128, r - j0);
+    const uint16_t* d = down + (int64_t)j0 * ld_down;
+    uint16_t* uo = u + j0;
+    const int rb = (rr + 31) / 32;
+    switch (rb) {
+      case 1: hipLaunchKernelGGL(hf::lowrank_down_kernel<1>, dim3(blocks), dim3(256), 0, s, x, ldx, d, ld_down, uo, ldu, (int)M, (int)K, rr); break;
+      case 2: hipLaunchKernelGGL(hf::lowrank_down_kernel<2>, dim3(blocks), dim3(256), 0, s, x, ldx, d, ld_down, uo, ldu, (int)M, (int)K, rr); break;
+      case 3: hipLaunchKernelGGL(hf::lowrank_down_kernel<3>, dim3(blocks), dim3(256), 0, s, x, ldx, d, ld_down, uo, ldu, (int)M, (int)K, rr); break;
+      default: hipLaunchKernelGGL(hf::lowrank_down_kernel<4>, dim3(blocks), dim3(256), 0, s, x, ldx, d, ld_down, uo, ldu, (int)M, (int)K, rr); break;
+    }
+    const int st = launch_status();
+    if (st != HF_OK) return st;
+  }
+  return HF_OK;
+}
+
+int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
+                   const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
+                   uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hf_stream_t stream) {
+  if (M == 0 || N == 0) return (M < 0 || N < 0) ? HF_ERR_ARGUMENT : HF_OK;
+  int st = check_gemm_operands(q, ldq, w, ldw, M, N, K);
+  if (st != HF_OK) return st;
+  if (!sx || !sw || !y || ldy < N || r < 0) return HF_ERR_ARGUMENT;
+  if (!aligned(y, 8)) return HF_ERR_ALIGNMENT;
+  if (r > 0) {
+    if (!u || !up || ldu < r || ld_up < r) return HF_ERR_ARGUMENT;
+    if ((r % 8) || !aligned(u, 16) || !aligned(up, 16) || (ldu % 8) || (ld_up % 8)) return HF_ERR_ALIGNMENT;
+  }
+  hf::GemmArgs a{};
+  a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.sx = sx; a.sw = sw;
+  a.u = r > 0 ? u : nullptr; a.ldu = ldu; a.up = r > 0 ? up : nullptr; a.ldup = ld_up; a.r = r;
+  a.bias = bias; a.out = y; a.ldo = ldy; a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  return launch_gemm(a, false, static_cast<hipStream_t>(stream));
+}
+
+int hf_int8_gemm_i32(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, int32_t* acc, int64_t ldacc,
+                     int64_t M, int64_t N, int64_t K, hf_stream_t stream) {
+  if (M == 0 || N == 0) return (M < 0 || N < 0) ? HF_ERR_ARGUMENT : HF_OK;
+  int st = check_gemm_operands(q, ldq, w, ldw, M, N, K);
+  if (st != HF_OK) return st;
+  if (!acc || ldacc < N) return HF_ERR_ARGUMENT;
+  if (!aligned(acc, 16)) return HF_ERR_ALIGNMENT;
+  hf::GemmArgs a{};
+  a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.out = acc; a.ldo = ldacc;
+  a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  return launch_gemm(a, true, static_cast<hipStream_t>(stream));
+}
+
+int hf_convrot_linear(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* sw,
+                      const uint16_t* down, int64_t ld_down, const uint16_t* up, int64_t ld_up, int32_t r,
+                      const uint16_t* bias, int32_t group, int8_t* q_ws, float* sx_ws, uint16_t* u_ws, uint16_t* y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, hf_stream_t stream) {
+  int st = hf_rotate_quant(x, ldx, q_ws, K, sx_ws, M, K, group, stream);
+  if (st != HF_OK) return st;
+  if (r > 0) {
+    st = hf_lowrank_down(x, ldx, down, ld_down, u_ws, r, M, K, r, stream);
+    if (st != HF_OK) return st;
+  }
+  return hf_int8_linear(q_ws, K, w, ldw, sx_ws, sw, u_ws, r, up, ld_up, r, bias, y, ldy, M, N, K, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,191 @@
+// Online block-Hadamard rotation + per-token absmax INT8 quantization (one pass over x).
+//
+// Replaces the reference's `rotate_quant` (src/hyperflow_h3_flash/int8.py:194-221, host 326-344) with the
+// arithmetic of its torch path (int8.py:176-178):
+//   xr = bf16(x @ blockdiag(R))   R = regular Hadamard of order G = 4^n, entries +-2^-n
+//   sx = max(absmax_row(xr), 1e-12) / 127          (fp32, correctly rounded division)
+//   xq = clamp(rint(xr / sx), -127, 127)           (fp32, correctly rounded division, ties to even)
+//
+// The rotation is the unnormalised radix-4 butterfly H4 v = S - 2 reverse(v) (S = sum of the four), applied along
+// each base-4 digit of the in-group index, in fp64. Every product with +-1 and every partial sum is exact in fp64
+// whenever a group's nonzero inputs span at most 33 binades, so the single rounding to bf16 below is the rounding
+// of the exact sum. The 2^-n normalisation is a power of two and is folded into the scale.
+//
+// Layout: one wave processes one row. A row is walked in tiles of 1024 elements; lane p holds the 16 consecutive
+// elements 16p..16p+15 (a "pencil", two 16-byte loads). Digits 0 and 1 (bits 0-3 of the index) are transformed in
+// registers. For G >= 64 the fp64 pencils go through LDS once so that each lane holds 16 values along digits 2
+// and 3, transformed in registers again. The bf16-rounded values wait in a per-wave row buffer in LDS until the
+// row's absmax is known, then each lane quantizes 16 consecutive values and writes 16 bytes.
+#include "common.h"
+
+namespace hf {
+
+constexpr int kRqTile = 1024;                            // elements per wave step (64 lanes x 16)
+constexpr int kRqStride = 18;                            // doubles per pencil in the transpose scratch (16 + pad)
+constexpr int kRqScratchBytes = 64 * kRqStride * 8;      // 9216 bytes per wave
+
+__device__ __forceinline__ void h4(double& a, double& b, double& c, double& d) {
+  double s = (a + b) + (c + d);
+  double na = fma(-2.0, d, s), nb = fma(-2.0, c, s), nc = fma(-2.0, b, s), nd = fma(-2.0, a, s);
+  a = na;
+  b = nb;
+  c = nc;
+  d = nd;
+}
+
+// Radix-4 stage along the 16-entry array with digit stride S (1 or 4).
+template <int S>
+__device__ __forceinline__ void h4_stage(double (&v)[16]) {
+#pragma unroll
+  for (int base = 0; base < 16; ++base) {
+    if ((base / S) % 4 == 0) h4(v[base], v[base + S], v[base + 2 * S], v[base + 3 * S]);
+  }
+}
+
+size_t rotate_quant_lds_bytes(int waves, int K) { return (size_t)waves * (kRqScratchBytes + 2 * (size_t)K); }
+
+template <int LOG4G>
+__global__ __launch_bounds__(256) void rotate_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                           int8_t* __restrict__ q, int64_t ldq,
+                                                           float* __restrict__ s, int64_t M, int K) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int waves = blockDim.x >> 6;
+  unsigned char* mine = smem + (size_t)wave * (kRqScratchBytes + 2 * (size_t)K);
+  double* scratch = reinterpret_cast<double*>(mine);
+  uint16_t* rowbuf = reinterpret_cast<uint16_t*>(mine + kRqScratchBytes);
+  const int ntiles = (K + kRqTile - 1) / kRqTile;
+
+  for (int64_t row = (int64_t)blockIdx.x * waves + wave; row < M; row += (int64_t)gridDim.x * waves) {
+    const uint16_t* xrow = x + row * ldx;
+    float amax = 0.0f;
+
+    uint4 nxt0 = make_uint4(0, 0, 0, 0), nxt1 = nxt0;
+    if (lane * 16 < K) {
+      nxt0 = *reinterpret_cast<const uint4*>(xrow + lane * 16);
+      nxt1 = *reinterpret_cast<const uint4*>(xrow + lane * 16 + 8);
+    }
+    for (int t = 0; t < ntiles; ++t) {
+      const int e0 = t * kRqTile + lane * 16;
+      const uint4 cur0 = nxt0, cur1 = nxt1;
+      if (t + 1 < ntiles) {
+        const int e1 = e0 + kRqTile;
+        nxt0 = make_uint4(0, 0, 0, 0);
+        nxt1 = nxt0;
+        if (e1 < K) {
+          nxt0 = *reinterpret_cast<const uint4*>(xrow + e1);
+          nxt1 = *reinterpret_cast<const uint4*>(xrow + e1 + 8);
+        }
+      }
+      double v[16];
+      const uint32_t w[8] = {cur0.x, cur0.y, cur0.z, cur0.w, cur1.x, cur1.y, cur1.z, cur1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[2 * i] = (double)bf16_lo(w[i]);
+        v[2 * i + 1] = (double)bf16_hi(w[i]);
+      }
+      if constexpr (LOG4G >= 1) h4_stage<1>(v);
+      if constexpr (LOG4G >= 2) h4_stage<4>(v);
+
+      if constexpr (LOG4G <= 2) {
+        // Values are in natural order: round, track the absmax, park 16 bf16 in the row buffer.
+        uint32_t packed[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float lo = round_f64_to_bf16_value(v[2 * i]);
+          float hi = round_f64_to_bf16_value(v[2 * i + 1]);
+          amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
+          packed[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+        }
+        if (e0 < K) {
+          uint4* dst = reinterpret_cast<uint4*>(rowbuf + e0);
+          dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+          dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+        }
+      } else {
+        // Transpose the fp64 pencils through LDS so each lane holds 16 values along digits 2 (and 3).
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          double2 pr;
+          pr.x = v[2 * i];
+          pr.y = v[2 * i + 1];
+          *reinterpret_cast<double2*>(scratch + lane * kRqStride + 2 * i) = pr;
+        }
+        wave_lds_sync();
+        int base_elem;
+        bool valid;
+        if constexpr (LOG4G == 4) {
+          // lane = 16*gi + b; v[a] = pencil (16*gi + a), column b; element 256*gi + 16*a + b
+          const int gi = lane >> 4, b = lane & 15;
+#pragma unroll
+          for (int a = 0; a < 16; ++a) v[a] = scratch[(16 * gi + a) * kRqStride + b];
+          base_elem = t * kRqTile + 256 * gi + b;
+          valid = t * kRqTile + 256 * gi < K;
+          h4_stage<1>(v);
+          h4_stage<4>(v);
+        } else {
+          // lane = 4*gi + cq; v[4a + cc] = pencil (4*gi + a), column 4*cq + cc; element 64*gi + 16*a + 4*cq + cc
+          const int gi = lane >> 2, cq = lane & 3;
+#pragma unroll
+          for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) v[4 * a + cc] = scratch[(4 * gi + a) * kRqStride + 4 * cq + cc];
+          base_elem = t * kRqTile + 64 * gi + 4 * cq;
+          valid = t * kRqTile + 64 * gi < K;
+          h4_stage<4>(v);
+        }
+        wave_lds_sync();  // scratch is rewritten by the next tile
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float r = round_f64_to_bf16_value(v[i]);
+          amax = fmaxf(amax, fabsf(r));
+          if (valid) {
+            const int e = (LOG4G == 4) ? base_elem + 16 * i : base_elem + 16 * (i >> 2) + (i & 3);
+            rowbuf[e] = (uint16_t)(__float_as_uint(r) >> 16);
+          }
+        }
+      }
+    }
+
+    amax = wave_max(amax);
+    // amax of xr = amax of the unnormalised sums * 2^-n (exact); then the reference's clamp and division.
+    const float sx = fmaxf(ldexpf(amax, -2 * LOG4G), 1e-12f) / 127.0f;
+    const float d = ldexpf(sx, 2 * LOG4G);  // (t * 2^n) / (sx * 2^n) == xr / sx exactly
+    if (lane == 0) s[row] = sx;
+    wave_lds_sync();
+
+    int8_t* qrow = q + row * ldq;
+    for (int t = 0; t < ntiles; ++t) {
+      const int e0 = t * kRqTile + lane * 16;
+      if (e0 >= K) continue;
+      const uint4* src = reinterpret_cast<const uint4*>(rowbuf + e0);
+      const uint4 a = src[0], b = src[1];
+      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      uint32_t out[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t pair = w[2 * i + h];
+          float r0 = rintf(bf16_lo(pair) / d);
+          float r1 = rintf(bf16_hi(pair) / d);
+          r0 = fminf(fmaxf(r0, -127.0f), 127.0f);
+          r1 = fminf(fmaxf(r1, -127.0f), 127.0f);
+          word |= ((uint32_t)((int)r0 & 0xff) | ((uint32_t)((int)r1 & 0xff) << 8)) << (16 * h);
+        }
+        out[i] = word;
+      }
+      *reinterpret_cast<uint4*>(qrow + e0) = make_uint4(out[0], out[1], out[2], out[3]);
+    }
+    wave_lds_sync();  // the row buffer is rewritten by the next row
+  }
+}
+
+template __global__ void rotate_quant_kernel<1>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
+template __global__ void rotate_quant_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
+template __global__ void rotate_quant_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
+template __global__ void rotate_quant_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
+
+}  // namespace hf

@@ -1,0 +1,302 @@
+"""INT8 W8A8 linears with a Hadamard-rotated input dimension, on MI355X (gfx950) HIP kernels.
+
+A drop-in for the reference's ``hyperflow_h3_flash.int8`` (src/hyperflow_h3_flash/int8.py): the same
+``Int8RotLinear(in_features, out_features, group)`` constructor, ``forward``, ``keep_input`` sharing and state dict
+(``qweight`` int8 [N, K], ``wscale`` fp32 [N], frozen parameters, no buffers), the same ``regular_hadamard`` /
+``hadamard_factors`` helpers and the same ``KERNEL_OPTIONS`` / ``set_kernel_options`` / ``resolve_int8_gemm`` API.
+
+``y = (q(x R) @ qweight^T) * s_x * wscale`` with ``R = blockdiag(regular Hadamard of order group)``. The device path
+is two launches of the hand-written kernels in ``csrc/`` (through the C ABI of include/hf_convrot.h): the rotation
++ per-token quantization, then the INT8 MFMA GEMM with the rescale fused in its epilogue. The arithmetic is that of
+the reference's torch path (int8.py:173-179): the rotated activation is rounded to bf16 before the absmax, and the
+scale and code divisions are true fp32 divisions; the int32 accumulators are exact.
+
+Extension (opt-in, adds no tensors when unused): ``rank > 0`` adds the low-rank branch of the reference's
+``LowRankLinear`` (``up(down(x))``, src/hyperflow_h3_flash/transformer.py:48-58) and ``bias=True`` a bf16 bias, both
+fused into the GEMM epilogue: ``y = bf16((acc*sx)*wscale + bf16(x @ down^T) @ up^T + bias)``.
+
+There is one backend. Every ``int8_gemm`` choice the reference accepts resolves to it, and both ``rotate_quant``
+choices run the same exactly-rounded rotation (the reference's "factored" kernel differs from its dense one by
+rare one-code roundings, int8.py:23-25; this build always produces the torch-path rounding). Inputs must be on a
+ROCm device; there is no CPU compute path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+from types import SimpleNamespace
+from typing import Any, ClassVar
+
+import torch
+from torch import Tensor, nn
+
+from . import _native
+
+#: Run-time kernel choices accepted for API compatibility with the reference (int8.py:37-39).
+INT8_GEMMS = ("auto", "triton", "cublas", "sgl", "bf16")
+ROTATE_QUANTS = ("dense", "factored")
+
+#: The single backend every choice runs on.
+BACKEND = "hip-gfx950"
+
+#: Run-time kernel choices for every `Int8RotLinear` (int8.py:45-46).
+KERNEL_OPTIONS: dict[str, Any] = {"int8_gemm": "auto", "rotate_quant": "dense"}
+
+
+def set_kernel_options(*, int8_gemm: str | None = None, rotate_quant: str | None = None) -> None:
+    """Validate and store kernel choices (int8.py:49-57): ValueError for names outside the reference's sets."""
+    if int8_gemm is not None:
+        if int8_gemm not in INT8_GEMMS:
+            raise ValueError(f"int8_gemm must be one of {INT8_GEMMS}, got {int8_gemm!r}")
+        KERNEL_OPTIONS["int8_gemm"] = int8_gemm
+    if rotate_quant is not None:
+        if rotate_quant not in ROTATE_QUANTS:
+            raise ValueError(f"rotate_quant must be one of {ROTATE_QUANTS}, got {rotate_quant!r}")
+        KERNEL_OPTIONS["rotate_quant"] = rotate_quant
+
+
+def resolve_int8_gemm(device: torch.device | None = None) -> str:
+    """The GEMM ``KERNEL_OPTIONS["int8_gemm"]`` runs as (int8.py:85-97): always the gfx950 HIP kernel here."""
+    return BACKEND
+
+
+@functools.cache
+def regular_hadamard(group: int) -> Tensor:
+    """``kron(H4 / 2, ..., H4 / 2)`` of size ``group`` (a power of 4): orthonormal, symmetric, rows sum to one.
+
+    Built in float64 and returned as float32, like int8.py:100-109; ValueError when ``group`` is not a power of 4."""
+    h4 = torch.tensor([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=torch.float64) / 2
+    h, n = torch.ones(1, 1, dtype=torch.float64), 1
+    while n < group:
+        h, n = torch.kron(h, h4), n * 4
+    if n != group:
+        raise ValueError(f"Hadamard group {group} is not a power of 4")
+    return h.float()
+
+
+def hadamard_factors(group: int) -> tuple[int, int] | None:
+    """``(GA, GB)`` with ``regular_hadamard(group) == kron(regular_hadamard(GA), regular_hadamard(GB))``, both at
+    least 16; None when ``group`` cannot be split that way (int8.py:112-119)."""
+    n = group.bit_length() - 1
+    if group < 256 or group != 1 << n or n % 2:
+        return None
+    ga = 4 ** (n // 4)
+    return ga, group // ga
+
+
+#: Groups the device rotation implements (powers of 4 up to 256 that divide K).
+DEVICE_GROUPS = (4, 16, 64, 256)
+
+
+def _check_group(group: int) -> None:
+    regular_hadamard(group)  # ValueError for a non-power of 4, as the reference raises at first use
+    if group not in DEVICE_GROUPS:
+        raise ValueError(f"Hadamard group {group} is not supported by the gfx950 kernels (supported: {DEVICE_GROUPS})")
+
+
+class Int8RotLinear(nn.Module):
+    """Bias-free W8A8 linear: ``y = (q(x R) @ qweight^T) * s_x * wscale``, ``R = blockdiag(regular Hadamard)``.
+
+    Linears that read one input (``to_q``, ``to_k``, ``to_v``) quantize it once: a layer with ``keep_input = True``
+    leaves its quantized input for the next layer, which reuses it if it receives the exact same, unmodified tensor.
+    Any other layer clears it, so nothing outlives the projections (int8.py:127-159).
+
+    ``rank`` and ``bias`` are this build's fused extension; with their defaults the module and its state dict are
+    exactly the reference's.
+    """
+
+    _last_input: ClassVar[dict[str, Any]] = {}
+
+    def __init__(self, in_features: int, out_features: int, group: int, *, rank: int = 0, bias: bool = False) -> None:
+        super().__init__()
+        if in_features % group:
+            raise ValueError(f"in_features {in_features} is not a multiple of the Hadamard group {group}")
+        if rank < 0:
+            raise ValueError(f"rank must be >= 0, got {rank}")
+        self.in_features, self.out_features, self.group = in_features, out_features, group
+        self.rank = rank
+        self.keep_input = False
+        # Parameters, not buffers: offload hooks move parameters back to the host (int8.py:143-145).
+        self.qweight = nn.Parameter(torch.zeros(out_features, in_features, dtype=torch.int8), requires_grad=False)
+        self.wscale = nn.Parameter(torch.ones(out_features, dtype=torch.float32), requires_grad=False)
+        if rank:
+            # LowRankLinear's layout (transformer.py:52-54): down.weight [rank, in], up.weight [out, rank].
+            self.down = nn.Linear(in_features, rank, bias=False, dtype=torch.bfloat16)
+            self.up = nn.Linear(rank, out_features, bias=False, dtype=torch.bfloat16)
+            for p in (self.down.weight, self.up.weight):
+                p.requires_grad_(False)
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_features, dtype=torch.bfloat16), requires_grad=False)
+        else:
+            self.bias = None
+
+    def extra_repr(self) -> str:
+        text = f"in_features={self.in_features}, out_features={self.out_features}, group={self.group}"
+        if self.rank:
+            text += f", rank={self.rank}"
+        if self.bias is not None:
+            text += ", bias=True"
+        return text
+
+    def _quantize(self, x: Tensor, x2: Tensor, kernels: SimpleNamespace) -> tuple[Tensor, Tensor]:
+        cache = Int8RotLinear._last_input
+        # Inference tensors (`torch.inference_mode`) have no version counter.
+        version = None if x.is_inference() else x._version
+        hit = cache.get("x") is x and cache.get("version") == version and cache.get("group") == self.group
+        quantized = cache["value"] if hit else kernels.rotate_quant(x2, self.group)
+        cache.clear()
+        if self.keep_input:
+            cache.update(x=x, version=version, group=self.group, value=quantized)
+        return quantized
+
+    def forward(self, x: Tensor) -> Tensor:
+        shape = x.shape
+        x2 = x.reshape(-1, self.in_features).to(torch.bfloat16).contiguous()
+        if not x2.is_cuda:
+            Int8RotLinear._last_input.clear()
+            raise RuntimeError(
+                f"Int8RotLinear runs on the gfx950 HIP kernels; move the module and its input to a ROCm device "
+                f"(input is on {x2.device})"
+            )
+        kernels = _kernels()
+        xq, sx = self._quantize(x, x2, kernels)
+        if self.rank:
+            u = kernels.lowrank_down(x2, self.down.weight)
+            y = kernels.int8_matmul(xq, self.qweight, sx, self.wscale, u=u, up=self.up.weight, bias=self.bias)
+        else:
+            y = kernels.int8_matmul(xq, self.qweight, sx, self.wscale, bias=self.bias)
+        return y.reshape(*shape[:-1], self.out_features).to(x.dtype)
+
+
+# ------------------------------------------------------------------------------------------------ device kernels
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _check(status: int, what: str) -> None:
+    if status == _native.HF_OK:
+        return
+    text = _native.status_text(status)
+    if status in (-1, -2, -3, -5):
+        raise ValueError(f"{what}: {text}")
+    raise RuntimeError(f"{what}: {text}")
+
+
+def _same_device(device: torch.device, *tensors: Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and t.device != device:
+            raise ValueError(f"tensor on {t.device}, expected {device}")
+
+
+def rotate_quant(x: Tensor, group: int) -> tuple[Tensor, Tensor]:
+    """(int8 codes [M, K], fp32 per-token scales [M]) of ``x`` (bf16 [M, K], rows contiguous), int8.py:326-344."""
+    _check_group(group)
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("rotate_quant expects a bf16 [M, K] tensor with contiguous rows")
+    M, K = x.shape
+    q = torch.empty(M, K, device=x.device, dtype=torch.int8)
+    s = torch.empty(M, device=x.device, dtype=torch.float32)
+    with torch.cuda.device(x.device):
+        status = _native.library().hf_rotate_quant(_ptr(x), x.stride(0), _ptr(q), q.stride(0), _ptr(s), M, K, group,
+                                                   _stream(x.device))
+    _check(status, "hf_rotate_quant")
+    return q, s
+
+
+def lowrank_down(x: Tensor, down: Tensor) -> Tensor:
+    """``bf16(x @ down^T)`` for x bf16 [M, K] and down bf16 [r, K] (LowRankLinear.down, transformer.py:57)."""
+    M, K = x.shape
+    r = down.shape[0]
+    _same_device(x.device, down)
+    down = down.to(torch.bfloat16).contiguous()
+    u = torch.empty(M, r, device=x.device, dtype=torch.bfloat16)
+    with torch.cuda.device(x.device):
+        status = _native.library().hf_lowrank_down(_ptr(x), x.stride(0), _ptr(down), down.stride(0), _ptr(u),
+                                                   u.stride(0), M, K, r, _stream(x.device))
+    _check(status, "hf_lowrank_down")
+    return u
+
+
+def _pad_rank(u: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
+    # The kernel reads the rank in 8-wide chunks; zero columns add exact zeros (transformer.py:60-73).
+    r = u.shape[1]
+    pad = -r % 8
+    if pad:
+        u = torch.nn.functional.pad(u, (0, pad))
+        up = torch.nn.functional.pad(up, (0, pad))
+    return u.contiguous(), up.contiguous()
+
+
+def int8_matmul(a: Tensor, b: Tensor, sa: Tensor, sb: Tensor, *, u: Tensor | None = None, up: Tensor | None = None,
+                bias: Tensor | None = None) -> Tensor:
+    """``bf16((f32(a @ b^T) * sa) * sb [+ u @ up^T] [+ bias])`` for a int8 [M, K], b int8 [N, K] (int8.py:376-390)."""
+    M, K = a.shape
+    N = b.shape[0]
+    if b.shape[1] != K:
+        raise ValueError(f"K mismatch: {a.shape} vs {b.shape}")
+    _same_device(a.device, b, sa, sb, u, up, bias)
+    a, b = a.contiguous(), b.contiguous()
+    sa = sa.to(torch.float32).contiguous()
+    sb = sb.to(torch.float32).contiguous()
+    r = 0
+    if u is not None:
+        u, up = _pad_rank(u.to(torch.bfloat16), up.to(torch.bfloat16))
+        r = u.shape[1]
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    c = torch.empty(M, N, device=a.device, dtype=torch.bfloat16)
+    with torch.cuda.device(a.device):
+        status = _native.library().hf_int8_linear(
+            _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(sa), _ptr(sb),
+            _ptr(u), u.stride(0) if u is not None else 0, _ptr(up), up.stride(0) if up is not None else 0, r,
+            _ptr(bias), _ptr(c), c.stride(0), M, N, K, _stream(a.device))
+    _check(status, "hf_int8_linear")
+    return c
+
+
+def int8_gemm_i32(a: Tensor, b: Tensor) -> Tensor:
+    """The exact int32 accumulator ``a @ b^T`` (the sum inside int8.py:302-306), for parity checks."""
+    M, K = a.shape
+    N = b.shape[0]
+    _same_device(a.device, b)
+    a, b = a.contiguous(), b.contiguous()
+    acc = torch.empty(M, N, device=a.device, dtype=torch.int32)
+    with torch.cuda.device(a.device):
+        status = _native.library().hf_int8_gemm_i32(_ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(acc),
+                                                    acc.stride(0), M, N, K, _stream(a.device))
+    _check(status, "hf_int8_gemm_i32")
+    return acc
+
+
+@functools.cache
+def _kernels() -> SimpleNamespace:
+    """The device kernels as a namespace shaped like the reference's ``_kernels()`` (int8.py:182-398).
+
+    Raises RuntimeError when the HIP library is missing: there is no other backend to fall back to."""
+    _native.library()
+    return SimpleNamespace(
+        rotate_quant=rotate_quant,
+        int8_matmul=int8_matmul,
+        lowrank_down=lowrank_down,
+        int8_gemm_i32=int8_gemm_i32,
+        backend=BACKEND,
+    )
+
+
+__all__ = [
+    "INT8_GEMMS",
+    "KERNEL_OPTIONS",
+    "ROTATE_QUANTS",
+    "Int8RotLinear",
+    "hadamard_factors",
+    "regular_hadamard",
+    "resolve_int8_gemm",
+    "set_kernel_options",
+]

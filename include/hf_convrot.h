@@ -1,0 +1,99 @@
+/*
+ * hf_convrot — C ABI of the MI355X (gfx950) INT8 "convrot" linear: a W8A8 linear whose input is rotated by a
+ * block-diagonal regular Hadamard matrix and quantized per token.
+ *
+ * Every entry point takes plain device pointers, element strides (leading dimensions, in elements) and sizes,
+ * launches on `stream` (a hipStream_t; NULL is the legacy default stream) of the current HIP device, never
+ * synchronizes, never allocates, and returns HF_OK or a negative HF_ERR_* code. Callers own every buffer.
+ *
+ * bf16 tensors are passed as `uint16_t*` bit patterns. All matrices are row-major with the reduction dimension K
+ * contiguous ("NT" GEMM: activations [M, K], weights [N, K]).
+ *
+ * Reference interfaces replaced (Video-Rebirth/hyperflow-h3-flash, src/hyperflow_h3_flash/):
+ *   hf_rotate_quant   <- `_kernels().rotate_quant(x2, group)`              int8.py:326-344 (kernel int8.py:194-221)
+ *   hf_int8_linear    <- `_kernels().int8_matmul(a, b, sa, sb)`            int8.py:376-390 (kernel int8.py:283-313)
+ *                        extended with the low-rank + bias epilogue of      transformer.py:57-58
+ *   hf_lowrank_down   <- `LowRankLinear.down(x)` (bf16 nn.Linear)          transformer.py:57-58
+ *   hf_int8_gemm_i32  <- the int32 accumulator of `int8_mm_kernel`         int8.py:302-306 (torch._int_mm, :362)
+ *   hf_convrot_linear <- `Int8RotLinear.forward` device branch             int8.py:161-171
+ */
+#ifndef HF_CONVROT_H
+#define HF_CONVROT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HF_OK 0
+#define HF_ERR_ARGUMENT (-1)  /* null pointer, negative size, stride smaller than the row */
+#define HF_ERR_GROUP (-2)     /* group is not 4, 16, 64 or 256, or does not divide K */
+#define HF_ERR_ALIGNMENT (-3) /* a pointer or stride breaks the 16-byte vector-access rules below */
+#define HF_ERR_LAUNCH (-4)    /* the HIP launch failed (hipGetLastError) */
+#define HF_ERR_SIZE (-5)      /* a size exceeds what the kernels index (see each function) */
+
+typedef void* hf_stream_t; /* hipStream_t */
+
+/* Library version string, e.g. "hf_convrot 0.1.0 gfx950". */
+const char* hf_version(void);
+
+/* Human-readable text for a status code. */
+const char* hf_strerror(int status);
+
+/*
+ * Rotate and quantize activations (one pass over x):
+ *   xr = bf16(x[m, g*G:(g+1)*G] @ H_G)   exact sum, rounded once to nearest even   (int8.py:176)
+ *   sx[m] = max(max_k |xr[m, k]|, 1e-12) / 127                                    (int8.py:177)
+ *   q[m, k] = clamp(rint(xr[m, k] / sx[m]), -127, 127)                             (int8.py:178)
+ * x: bf16 [M, ldx]; q: int8 [M, ldq]; sx: fp32 [M].
+ * Requires: group in {4, 16, 64, 256} dividing K; K % 16 == 0; x and q 16-byte aligned; ldx % 8 == 0;
+ * ldq % 16 == 0; K <= 77312.
+ */
+int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int64_t K,
+                    int32_t group, hf_stream_t stream);
+
+/*
+ * Low-rank down projection u = bf16(x @ down^T) (LowRankLinear's bf16 intermediate, transformer.py:57-58).
+ * x: bf16 [M, ldx]; down: bf16 [r, ld_down] (nn.Linear(K, r).weight); u: bf16 [M, ldu].
+ * Requires: K % 16 == 0; x, down 16-byte aligned; ldx % 8 == 0; ld_down % 8 == 0; u 8-byte aligned.
+ */
+int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_t ld_down, uint16_t* u,
+                    int64_t ldu, int64_t M, int64_t K, int32_t r, hf_stream_t stream);
+
+/*
+ * Fused INT8 linear:
+ *   acc = q @ w^T (exact int32)
+ *   y = bf16((f32(acc) * sx[m]) * sw[n] + sum_j u[m, j] * up[n, j] + bias[n])
+ * With r == 0 and bias == NULL this is bitwise the reference's `bf16((acc * sx) * wscale)` (int8.py:179).
+ * q: int8 [M, ldq]; w: int8 [N, ldw] (qweight); sx: fp32 [M]; sw: fp32 [N] (wscale);
+ * u: bf16 [M, ldu] or NULL; up: bf16 [N, ld_up] (LowRankLinear.up.weight) or NULL; r: rank (0 = none);
+ * bias: bf16 [N] or NULL; y: bf16 [M, ldy].
+ * Requires: K % 16 == 0; q, w 16-byte aligned; ldq, ldw multiples of 16; 256 * ldq and 256 * ldw < 2^31; y 8-byte aligned;
+ * when r > 0: r % 8 == 0, u and up 16-byte aligned, ldu and ld_up multiples of 8.
+ */
+int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
+                   const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
+                   uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hf_stream_t stream);
+
+/*
+ * The int32 accumulator alone: acc = q @ w^T (for parity checks). acc: int32 [M, ldacc], 16-byte aligned.
+ * Same operand rules as hf_int8_linear.
+ */
+int hf_int8_gemm_i32(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, int32_t* acc, int64_t ldacc,
+                     int64_t M, int64_t N, int64_t K, hf_stream_t stream);
+
+/*
+ * The whole layer on caller-provided workspaces: hf_rotate_quant into (q_ws [M, K], sx_ws [M]), then, when r > 0,
+ * hf_lowrank_down into u_ws [M, r], then hf_int8_linear into y. Same rules as the three calls.
+ */
+int hf_convrot_linear(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t ldw, const float* sw,
+                      const uint16_t* down, int64_t ld_down, const uint16_t* up, int64_t ld_up, int32_t r,
+                      const uint16_t* bias, int32_t group, int8_t* q_ws, float* sx_ws, uint16_t* u_ws, uint16_t* y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, hf_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HF_CONVROT_H */

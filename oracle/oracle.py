@@ -1,0 +1,257 @@
+"""ORACLE — test infrastructure only.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this module, and only as
+the checker. The product (``hyperflow_h3_flash_amd``) never imports it.
+
+A CPU restatement of the reference's INT8 convrot linear (``Int8RotLinear._forward_torch``,
+src/hyperflow_h3_flash/int8.py:173-179) backed by ``convrot_oracle.c`` (built by ``oracle/Makefile``), plus the
+numpy closed forms the tests pin it with:
+
+* ``regular_hadamard`` — int8.py:100-109 (``kron(H4/2, ...)``, float64);
+* ``hadamard_factors`` — int8.py:112-119;
+* ``quantize_weight`` — the checkpoint quantizer of tests/test_int8.py:31-36 (float64);
+* ``rotate`` / ``quantize`` / ``int8_gemm`` / ``epilogue`` — int8.py:176-179 step by step;
+* ``lowrank_down`` / ``fused_epilogue`` — LowRankLinear (src/hyperflow_h3_flash/transformer.py:57-58) and a bias;
+* ``composition`` — the reference's own composition ``Int8RotLinear(x) + LowRankLinear(x) + bias`` in bf16 tensor
+  arithmetic, which is what the fused extension is graded against.
+
+Every array crossing into C is a contiguous numpy array; bf16 tensors are carried as ``uint16`` bit patterns.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from functools import lru_cache
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+
+def build() -> str:
+    """Compile ``convrot_oracle.c`` with gcc (oracle/Makefile). Returns the library path."""
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+    return _LIB_PATH
+
+
+@lru_cache(maxsize=None)
+def _lib() -> ctypes.CDLL:
+    if not os.path.exists(_LIB_PATH):
+        build()
+    lib = ctypes.CDLL(_LIB_PATH)
+    p, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.oracle_regular_hadamard.argtypes = [i32, p]
+    lib.oracle_rotate.argtypes = [p, i64, i64, i32, p, i32]
+    lib.oracle_quantize.argtypes = [p, i64, i64, p, p]
+    lib.oracle_int8_gemm.argtypes = [p, p, i64, i64, i64, p]
+    lib.oracle_epilogue.argtypes = [p, p, p, i64, i64, p]
+    lib.oracle_lowrank_down.argtypes = [p, p, i64, i64, i64, p]
+    lib.oracle_fused_epilogue.argtypes = [p, p, p, p, p, i64, p, i64, i64, p]
+    lib.oracle_convrot_linear.argtypes = [p, p, p, i64, i64, i64, i32, p, p, p, p, p]
+    lib.oracle_f64_to_bf16.argtypes = [ctypes.c_double]
+    lib.oracle_f64_to_bf16.restype = ctypes.c_uint16
+    lib.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+    lib.oracle_f32_to_bf16.restype = ctypes.c_uint16
+    return lib
+
+
+def _ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags.c_contiguous, "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ----------------------------------------------------------------------------------------------------- bf16 helpers
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """uint16 bf16 bit patterns -> float32 values (exact)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even (NaN kept quiet)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def f64_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float64 -> bf16 bits rounded once (no fp32 double rounding), via the C routine."""
+    lib = _lib()
+    flat = np.ascontiguousarray(x, dtype=np.float64).ravel()
+    out = np.fromiter((lib.oracle_f64_to_bf16(float(v)) for v in flat), dtype=np.uint16, count=flat.size)
+    return out.reshape(np.shape(x))
+
+
+# ------------------------------------------------------------------------------------------- Hadamard closed forms
+
+
+def regular_hadamard(group: int) -> np.ndarray:
+    """``kron(H4/2, ..., H4/2)`` of size ``group`` in float64 (int8.py:100-109). ValueError unless a power of 4."""
+    h4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.float64) / 2
+    h, n = np.ones((1, 1)), 1
+    while n < group:
+        h, n = np.kron(h, h4), n * 4
+    if n != group:
+        raise ValueError(f"Hadamard group {group} is not a power of 4")
+    return h
+
+
+def regular_hadamard_c(group: int) -> np.ndarray:
+    """The C oracle's sign-rule construction of the same matrix (digit sums of 3 give -1)."""
+    out = np.empty((group, group), dtype=np.float64)
+    if _lib().oracle_regular_hadamard(group, _ptr(out)) != 0:
+        raise ValueError(f"Hadamard group {group} is not a power of 4")
+    return out
+
+
+def hadamard_factors(group: int) -> tuple[int, int] | None:
+    """``(GA, GB)`` with ``kron(H_GA, H_GB) == H_group``, both >= 16; None otherwise (int8.py:112-119)."""
+    n = group.bit_length() - 1
+    if group < 256 or group != 1 << n or n % 2:
+        return None
+    ga = 4 ** (n // 4)
+    return ga, group // ga
+
+
+def quantize_weight(weight: np.ndarray, group: int) -> tuple[np.ndarray, np.ndarray]:
+    """The checkpoint format of tests/test_int8.py:31-36: ``qweight = round(W R / wscale)``, in float64."""
+    w = np.asarray(weight, dtype=np.float64)
+    k = w.shape[1]
+    h = regular_hadamard(group)
+    rotated = (w.reshape(w.shape[0], k // group, group) @ h).reshape(w.shape)
+    wscale = np.abs(rotated).max(axis=1) / 127.0
+    q = np.clip(np.round(rotated / wscale[:, None]), -127, 127).astype(np.int8)
+    return q, wscale.astype(np.float32)
+
+
+# ------------------------------------------------------------------------------------------------- the restatement
+
+
+def rotate(x_bits: np.ndarray, group: int, *, force_exact: bool = False) -> np.ndarray:
+    """``bf16(x.view(M, K/G, G) @ R)`` with the sum computed exactly and rounded once (int8.py:176)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    m, k = x.shape
+    out = np.empty_like(x)
+    if _lib().oracle_rotate(_ptr(x), m, k, group, _ptr(out), int(force_exact)) != 0:
+        raise ValueError(f"bad rotation shape K={k} group={group}")
+    return out
+
+
+def quantize(xr_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per-token scale and int8 codes (int8.py:177-178). Returns (sx float32 [M], xq int8 [M, K])."""
+    xr = np.ascontiguousarray(xr_bits, dtype=np.uint16)
+    m, k = xr.shape
+    sx = np.empty(m, dtype=np.float32)
+    xq = np.empty((m, k), dtype=np.int8)
+    _lib().oracle_quantize(_ptr(xr), m, k, _ptr(sx), _ptr(xq))
+    return sx, xq
+
+
+def int8_gemm(xq: np.ndarray, qweight: np.ndarray) -> np.ndarray:
+    """Exact ``xq @ qweight^T`` as int32 [M, N] (int8.py:179). Raises if a sum leaves int32."""
+    a = np.ascontiguousarray(xq, dtype=np.int8)
+    b = np.ascontiguousarray(qweight, dtype=np.int8)
+    m, k = a.shape
+    n = b.shape[0]
+    acc = np.empty((m, n), dtype=np.int32)
+    if _lib().oracle_int8_gemm(_ptr(a), _ptr(b), m, n, k, _ptr(acc)) != 0:
+        raise OverflowError("int8 GEMM sum outside int32")
+    return acc
+
+
+def epilogue(acc: np.ndarray, sx: np.ndarray, wscale: np.ndarray) -> np.ndarray:
+    """``bf16((f32(acc) * sx) * wscale)`` (int8.py:179). Returns bf16 bits [M, N]."""
+    acc = np.ascontiguousarray(acc, dtype=np.int32)
+    m, n = acc.shape
+    y = np.empty((m, n), dtype=np.uint16)
+    _lib().oracle_epilogue(_ptr(acc), _ptr(np.ascontiguousarray(sx, np.float32)),
+                           _ptr(np.ascontiguousarray(wscale, np.float32)), m, n, _ptr(y))
+    return y
+
+
+def convrot_linear(x_bits: np.ndarray, qweight: np.ndarray, wscale: np.ndarray, group: int) -> dict:
+    """The whole bias-free reference layer. Returns ``{"xr", "sx", "xq", "acc", "y"}``."""
+    xr = rotate(x_bits, group)
+    sx, xq = quantize(xr)
+    acc = int8_gemm(xq, qweight)
+    return {"xr": xr, "sx": sx, "xq": xq, "acc": acc, "y": epilogue(acc, sx, wscale)}
+
+
+def lowrank_down(x_bits: np.ndarray, down_bits: np.ndarray) -> np.ndarray:
+    """``bf16(x @ down^T)``, the bf16 intermediate of LowRankLinear (transformer.py:57-58). down is [r, K]."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    d = np.ascontiguousarray(down_bits, dtype=np.uint16)
+    m, k = x.shape
+    r = d.shape[0]
+    u = np.empty((m, r), dtype=np.uint16)
+    _lib().oracle_lowrank_down(_ptr(x), _ptr(d), m, k, r, _ptr(u))
+    return u
+
+
+def fused_epilogue(acc, sx, wscale, u_bits=None, up_bits=None, bias_bits=None) -> np.ndarray:
+    """The fused extension's definition: ``bf16((f32(acc)*sx)*ws + u @ up^T + bias)`` rounded once."""
+    acc = np.ascontiguousarray(acc, dtype=np.int32)
+    m, n = acc.shape
+    r = 0 if u_bits is None else u_bits.shape[1]
+    y = np.empty((m, n), dtype=np.uint16)
+    _lib().oracle_fused_epilogue(
+        _ptr(acc), _ptr(np.ascontiguousarray(sx, np.float32)), _ptr(np.ascontiguousarray(wscale, np.float32)),
+        _ptr(None if u_bits is None else np.ascontiguousarray(u_bits, np.uint16)),
+        _ptr(None if up_bits is None else np.ascontiguousarray(up_bits, np.uint16)), r,
+        _ptr(None if bias_bits is None else np.ascontiguousarray(bias_bits, np.uint16)), m, n, _ptr(y))
+    return y
+
+
+def composition(y_int8_bits, x_bits, down_bits=None, up_bits=None, bias_bits=None) -> np.ndarray:
+    """``Int8RotLinear(x) + LowRankLinear(x) + bias`` in bf16 tensor arithmetic, as three reference modules compose:
+    the low-rank branch is ``bf16(bf16(x @ down^T) @ up^T)`` (transformer.py:57-58) and each ``+`` rounds to bf16."""
+    y = bf16_to_f32(y_int8_bits)
+    if down_bits is not None:
+        u = bf16_to_f32(lowrank_down(x_bits, down_bits)).astype(np.float64)
+        lr = bf16_to_f32(f64_to_bf16(u @ bf16_to_f32(up_bits).astype(np.float64).T))
+        y = bf16_to_f32(f32_to_bf16(y + lr))
+    if bias_bits is not None:
+        y = bf16_to_f32(f32_to_bf16(y + bf16_to_f32(bias_bits)[None, :]))
+    return f32_to_bf16(y)
+
+
+# ------------------------------------------------------------------------------------------------ seeded inputs
+
+
+def make_inputs(m: int, k: int, n: int, group: int, *, rank: int = 0, bias: bool = False,
+                outlier_frac: float = 0.01, outlier_scale: float = 20.0, seed: int = 0,
+                weight_dist: str = "uniform") -> dict:
+    """Deterministic synthetic inputs of the benchmark's distributions (numpy PCG64, one seed, fixed draw order:
+    x, outlier channels, qweight, wscale, down, up, bias).
+
+    x ~ N(0, 1) with ceil(p*K) outlier channels scaled in float32 before the single bf16 cast. ``weight_dist``
+    "uniform" draws qweight ~ U{-127..127} and wscale ~ U(1e-3, 1e-2); "quantized" draws W ~ 0.02 N(0,1) and
+    quantizes it with `quantize_weight` (the reference tests' recipe, tests/test_int8.py:93-99).
+    """
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    n_out = int(np.ceil(outlier_frac * k)) if outlier_frac > 0 else 0
+    if n_out:
+        cols = rng.choice(k, size=n_out, replace=False)
+        x[:, cols] *= np.float32(outlier_scale)
+    out = {"x": f32_to_bf16(x)}
+    if weight_dist == "uniform":
+        out["qweight"] = rng.integers(-127, 128, size=(n, k), dtype=np.int64).astype(np.int8)
+        out["wscale"] = rng.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+    else:
+        w = rng.standard_normal((n, k)) * 0.02
+        out["qweight"], out["wscale"] = quantize_weight(w, group)
+    if rank:
+        out["down"] = f32_to_bf16((rng.standard_normal((rank, k)) * 0.02).astype(np.float32))
+        out["up"] = f32_to_bf16((rng.standard_normal((n, rank)) * 0.02).astype(np.float32))
+    if bias:
+        out["bias"] = f32_to_bf16((rng.standard_normal(n) * 0.01).astype(np.float32))
+    return out

@@ -1,0 +1,73 @@
+"""The C ABI: the built library loads and exports every function include/hf_convrot.h declares, and argument checks
+reject bad calls before any HIP call. CPU only: no kernel is launched here."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from hyperflow_h3_flash_amd import _native
+
+HEADER = os.path.join(_native.REPO_DIR, "include", "hf_convrot.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(hf_\w+)\s*\(", text, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.fail(f"{_native.LIB_PATH} not built: run __graft_entry__.build()")
+    return _native.library()
+
+
+def test_header_and_binding_agree():
+    names = declared_functions()
+    assert sorted(names) == sorted(_native.SIGNATURES), names
+
+
+def test_library_exports_every_declared_function(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_status_text(lib):
+    assert lib.hf_version().decode().startswith("hf_convrot ")
+    assert "gfx950" in lib.hf_version().decode()
+    for code in (0, -1, -2, -3, -4, -5):
+        assert lib.hf_strerror(code)
+    assert lib.hf_strerror(-99) == b"unknown status"
+
+
+def test_argument_checks_reject_before_launching(lib):
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: every call below fails validation first
+    odd = ctypes.c_void_p((1 << 20) + 4)
+    null = None
+    # null pointers
+    assert lib.hf_rotate_quant(null, 256, fake, 256, fake, 4, 256, 256, null) == -1
+    # zero rows is a no-op success
+    assert lib.hf_rotate_quant(null, 256, null, 256, null, 0, 256, 256, null) == 0
+    # unsupported group / group not dividing K
+    assert lib.hf_rotate_quant(fake, 256, fake, 256, fake, 4, 256, 32, null) == -2
+    assert lib.hf_rotate_quant(fake, 320, fake, 320, fake, 4, 320, 256, null) == -2
+    # misaligned pointer, K not a multiple of 16
+    assert lib.hf_rotate_quant(odd, 256, fake, 256, fake, 4, 256, 256, null) == -3
+    assert lib.hf_rotate_quant(fake, 8, fake, 8, fake, 4, 8, 4, null) == -3
+    # GEMM: stride smaller than K, misaligned stride, low-rank rank not a multiple of 8
+    assert lib.hf_int8_linear(fake, 64, fake, 128, fake, fake, null, 0, null, 0, 0, null, fake, 64, 4, 64, 128,
+                              null) == -1
+    assert lib.hf_int8_linear(fake, 136, fake, 136, fake, fake, null, 0, null, 0, 0, null, fake, 64, 4, 64, 130,
+                              null) == -3
+    assert lib.hf_int8_linear(fake, 128, fake, 128, fake, fake, fake, 12, fake, 12, 12, null, fake, 64, 4, 64, 128,
+                              null) == -3
+    assert lib.hf_int8_gemm_i32(fake, 128, fake, 128, odd, 64, 4, 64, 128, null) == -3
+    assert lib.hf_lowrank_down(fake, 128, fake, 128, fake, 4, 4, 128, 8, null) == -1  # ldu < r
+    assert lib.hf_lowrank_down(fake, 128, fake, 128, fake, 8, 4, 120, 8, null) == -3  # K % 16
+    # sizes beyond the kernels' index range
+    assert lib.hf_int8_gemm_i32(fake, 1 << 24, fake, 128, fake, 64, 4, 64, 128, null) == -5

@@ -1,0 +1,278 @@
+"""The oracle pinned: against the reference's own golden vectors (tests/golden, written from the reference's
+``_forward_torch``), closed forms, brute force in exact rational arithmetic, and planted mistakes that these checks
+must catch. CPU only."""
+
+from __future__ import annotations
+
+import itertools
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from golden_utils import classify_rotation_mismatches, fixture_names, fraction_to_bf16, load_fixture
+
+FIXTURES = fixture_names()
+
+
+def test_fixtures_present():
+    assert len(FIXTURES) >= 7, FIXTURES
+
+
+# ----------------------------------------------------------------------------------------- Hadamard (int8.py:100-119)
+
+
+@pytest.mark.parametrize("group", [4, 16, 64, 256, 1024])
+def test_regular_hadamard_closed_form(oracle_lib, group):
+    h = oracle_lib.regular_hadamard(group)
+    np.testing.assert_array_equal(h, oracle_lib.regular_hadamard_c(group))
+    np.testing.assert_allclose(h @ h.T, np.eye(group), atol=1e-12)
+    np.testing.assert_array_equal(h, h.T)
+    np.testing.assert_allclose(h.sum(axis=1), np.ones(group), atol=1e-12)  # "rows sum to one"
+    assert set(np.unique(np.abs(h))) == {group ** -0.5}
+
+
+@pytest.mark.parametrize("group", [2, 8, 32, 128, 512])
+def test_regular_hadamard_rejects_non_powers_of_four(oracle_lib, group):
+    with pytest.raises(ValueError):
+        oracle_lib.regular_hadamard(group)
+    with pytest.raises(ValueError):
+        oracle_lib.regular_hadamard_c(group)
+
+
+@pytest.mark.parametrize("group", [256, 1024, 4096])
+def test_hadamard_factors_rebuild_the_rotation(oracle_lib, group):
+    ga, gb = oracle_lib.hadamard_factors(group)
+    assert ga >= 16 and gb >= 16
+    np.testing.assert_array_equal(np.kron(oracle_lib.regular_hadamard(ga), oracle_lib.regular_hadamard(gb)),
+                                  oracle_lib.regular_hadamard(group))
+
+
+def test_small_groups_have_no_factors(oracle_lib):
+    assert oracle_lib.hadamard_factors(16) is None and oracle_lib.hadamard_factors(64) is None
+
+
+# --------------------------------------------------------------------------------- the rotation (int8.py:176)
+
+
+def _bits(values) -> np.ndarray:
+    return oracle_lib_f32_to_bf16(np.asarray(values, dtype=np.float32))
+
+
+def oracle_lib_f32_to_bf16(a):
+    from oracle import oracle
+
+    return oracle.f32_to_bf16(a)
+
+
+@pytest.mark.parametrize("group", [4, 16, 64])
+def test_rotation_is_the_exact_sum_rounded_once(oracle_lib, group):
+    """Brute force in exact rational arithmetic, on inputs spanning up to ~250 binades, with zeros and signs."""
+    rng = np.random.default_rng(group)
+    rows = []
+    for _ in range(6):
+        mags = rng.standard_normal(group) * np.exp2(rng.integers(-60, 60, size=group).astype(np.float64))
+        mags[rng.random(group) < 0.1] = 0.0
+        rows.append(mags)
+    rows.append(np.exp2(rng.integers(-120, 120, size=group).astype(np.float64)) * rng.choice([-1, 1], size=group))
+    x = _bits(np.array(rows, dtype=np.float64).astype(np.float32))
+    got = oracle_lib.rotate(x, group, force_exact=True)
+    h = oracle_lib.regular_hadamard(group)
+    for r in range(x.shape[0]):
+        xv = [Fraction(float(v)) for v in oracle_lib.bf16_to_f32(x[r])]
+        for j in range(group):
+            exact = sum((xv[i] * Fraction(h[i, j]) for i in range(group)), Fraction(0))
+            assert fraction_to_bf16(exact) == int(got[r, j]), (r, j)
+
+
+def test_rotation_rounds_ties_to_even(oracle_lib):
+    # G=4: out_0 = (x0 + x1 + x2 - x3) / 2. (1 + 2^-8)/2 = 0.5 + 2^-9 is the midpoint between 0.5 (even) and
+    # 0.5 + 2^-8; (1 + 3*2^-8)/2 is the midpoint between 0.5 + 2^-8 (odd) and 0.5 + 2^-7 (even).
+    x = _bits([[1.0, 2.0**-8, 0.0, 0.0], [1.0, 3 * 2.0**-8, 0.0, 0.0]])
+    out = oracle_lib.bf16_to_f32(oracle_lib.rotate(x, 4, force_exact=True))
+    assert out[0, 0] == 0.5 and out[1, 0] == 0.5 + 2.0**-7
+    out_fast = oracle_lib.bf16_to_f32(oracle_lib.rotate(x, 4))
+    np.testing.assert_array_equal(out, out_fast)
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_rotation_fast_path_equals_exact_path(oracle_lib, name):
+    f = load_fixture(name)
+    x = f["x"][:16]
+    np.testing.assert_array_equal(oracle_lib.rotate(x, f["G"]), oracle_lib.rotate(x, f["G"], force_exact=True))
+
+
+# ------------------------------------------------------------------------------ quantization (int8.py:177-178)
+
+
+def test_quantize_zero_row_and_half_even_ties(oracle_lib):
+    # Row 0 all zero: clamp_min(1e-12) / 127. Row 1: amax 127 gives sx == 1 exactly, so xr / sx hits the halves.
+    xr = _bits([[0.0] * 8, [127.0, 2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5]])
+    sx, xq = oracle_lib.quantize(xr)
+    assert sx[0] == np.float32(np.float32(1e-12) / np.float32(127.0)) and not xq[0].any()
+    assert sx[1] == 1.0
+    assert xq[1].tolist() == [127, 2, 4, -2, -4, 0, 2, 0]
+
+
+def test_quantize_divides_rather_than_multiplying_by_the_reciprocal(oracle_lib):
+    # A value whose true quotient rounds differently from a * (1/s): search small integers for one.
+    found = None
+    for amax_q in range(100, 3000):
+        amax = np.float32(amax_q) * np.float32(2.0**-7)
+        s = np.float32(amax / np.float32(127.0))
+        inv = np.float32(np.float32(1.0) / s)
+        for num in range(1, 400):
+            a = np.float32(num) * np.float32(2.0**-7)
+            if a > amax:
+                break
+            if np.rint(np.float32(a / s)) != np.rint(np.float32(a * inv)):
+                found = (amax, a)
+                break
+        if found:
+            break
+    assert found, "no case separating division from reciprocal multiplication"
+    amax, a = found
+    xr = _bits([[amax, a]])
+    sx, xq = oracle_lib.quantize(xr)
+    assert xq[0, 1] == np.rint(np.float32(a / sx[0]))
+
+
+# ------------------------------------------------------------------------------------ GEMM and epilogue (int8.py:179)
+
+
+def test_int8_gemm_is_the_exact_integer_product(oracle_lib):
+    rng = np.random.default_rng(3)
+    a = rng.integers(-127, 128, size=(37, 300), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-127, 128, size=(29, 300), dtype=np.int64).astype(np.int8)
+    np.testing.assert_array_equal(oracle_lib.int8_gemm(a, b), a.astype(np.int64) @ b.astype(np.int64).T)
+    big = np.full((1, 140000), 127, dtype=np.int8)
+    with pytest.raises(OverflowError):
+        oracle_lib.int8_gemm(big, big)
+
+
+def _rn32(v: Fraction) -> Fraction:
+    """Round an exact rational to the nearest fp32 (ties to even), by exact arithmetic."""
+    if v == 0:
+        return v
+    e = abs(v).numerator.bit_length() - abs(v).denominator.bit_length()
+    if Fraction(2) ** e > abs(v):
+        e -= 1
+    quantum = Fraction(2) ** (e - 23)
+    return round(v / quantum) * quantum
+
+
+def test_epilogue_order_is_left_to_right(oracle_lib):
+    """int8.py:179 evaluates ``(acc * sx) * wscale``: two fp32 roundings in that order. Search for operands where
+    the other association ``acc * (sx * wscale)`` rounds to a different bf16, and check the oracle takes the
+    reference's order (computed here in exact rational arithmetic)."""
+    rng = np.random.default_rng(9)
+    n = 1 << 20
+    acc = rng.integers(-2**22, 2**22, size=n).astype(np.int32)
+    sx = rng.uniform(1e-3, 1e-1, size=n).astype(np.float32)
+    ws = rng.uniform(1e-3, 1e-2, size=n).astype(np.float32)
+    a32 = acc.astype(np.float32)
+    cand = np.nonzero(oracle_lib.f32_to_bf16((a32 * sx) * ws) != oracle_lib.f32_to_bf16(a32 * (sx * ws)))[0][:64]
+    left, right, picked = [], [], []
+    for i in cand:  # confirm each candidate in exact rational arithmetic
+        a, s_, w = Fraction(int(acc[i])), Fraction(float(sx[i])), Fraction(float(ws[i]))
+        lv, rv = fraction_to_bf16(_rn32(_rn32(a * s_) * w)), fraction_to_bf16(_rn32(a * _rn32(s_ * w)))
+        if lv != rv:
+            picked.append(i)
+            left.append(lv)
+    assert picked, "no operands separate the two association orders"
+    got = [int(oracle_lib.epilogue(acc[i:i + 1, None].copy(), sx[i:i + 1], ws[i:i + 1])[0, 0]) for i in picked]
+    assert got == left
+
+
+# -------------------------------------------------------------------------- pinned to the reference's own outputs
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_oracle_matches_reference_golden(oracle_lib, name):
+    f = load_fixture(name)
+    out = oracle_lib.convrot_linear(f["x"], f["qweight"], f["wscale"], f["G"])
+    mismatches, unexplained = classify_rotation_mismatches(f["x"], out["xr"], f["xr"], f["G"])
+    assert not unexplained, unexplained
+    assert mismatches <= max(2, 1e-5 * out["xr"].size), mismatches
+    np.testing.assert_array_equal(out["sx"], f["sx"])
+    np.testing.assert_array_equal(out["xq"], f["xq"])
+    np.testing.assert_array_equal(out["acc"], f["acc"])
+    np.testing.assert_array_equal(out["y"], f["y"])
+
+
+def test_composition_matches_reference_golden(oracle_lib):
+    f = load_fixture("composition")
+    np.testing.assert_array_equal(oracle_lib.lowrank_down(f["x"], f["down"]), f["u"])
+    comp = oracle_lib.composition(f["y"], f["x"], f["down"], f["up"], f["bias"])
+    np.testing.assert_array_equal(comp, f["y_composed"])
+
+
+def test_fused_definition_is_within_tolerance_of_the_composition(oracle_lib):
+    f = load_fixture("composition")
+    out = oracle_lib.convrot_linear(f["x"], f["qweight"], f["wscale"], f["G"])
+    u = oracle_lib.lowrank_down(f["x"], f["down"])
+    fused = oracle_lib.bf16_to_f32(oracle_lib.fused_epilogue(out["acc"], out["sx"], f["wscale"], u, f["up"],
+                                                             f["bias"]))
+    comp = oracle_lib.bf16_to_f32(f["y_composed"])
+    assert np.abs(fused - comp).max() / np.abs(comp).max() <= 1e-2
+
+
+# ------------------------------------------------------------------------ planted mistakes the checks must catch
+
+
+def _mutant_linear(oracle_lib, f, mistake):
+    """The oracle's arithmetic restated in numpy with one planted mistake."""
+    g, n = f["G"], int(np.log2(f["G"]) // 2)
+    x = oracle_lib.bf16_to_f32(f["x"]).astype(np.float64)
+    h = oracle_lib.regular_hadamard(g)
+    if mistake == "sign_rule":
+        i = np.arange(g)
+        neg = np.zeros((g, g), dtype=bool)
+        for t in range(n):
+            neg ^= ((((i[:, None] >> (2 * t)) & 3) + ((i[None, :] >> (2 * t)) & 3)) == 0)
+        h = np.where(neg, -1.0, 1.0) / 2**n
+    rot = (x.reshape(x.shape[0], -1, g) @ h).reshape(x.shape)
+    xr = rot.astype(np.float32) if mistake == "no_bf16_rounding" else oracle_lib.bf16_to_f32(
+        oracle_lib.f64_to_bf16(rot))
+    sx = (np.maximum(np.abs(xr).max(axis=1), np.float32(1e-12)) / np.float32(127.0)).astype(np.float32)
+    xq = np.clip(np.rint((xr / sx[:, None]).astype(np.float32)), -127, 127)
+    acc = (xq.astype(np.int64) @ f["qweight"].astype(np.int64).T).astype(np.float32)
+    y = (acc * sx[:, None]) * f["wscale"][None, :]
+    return oracle_lib.f32_to_bf16(y.astype(np.float32)), sx
+
+
+@pytest.mark.parametrize("mistake", ["sign_rule", "no_bf16_rounding"])
+def test_planted_mistakes_are_caught_by_the_golden_vectors(oracle_lib, mistake):
+    caught = 0
+    for name in ("cfg1_slice", "odd_tail", "cfg2_slice"):
+        f = load_fixture(name)
+        y, sx = _mutant_linear(oracle_lib, f, mistake)
+        caught += int((y != f["y"]).sum()) + int((sx != f["sx"]).sum())
+    assert caught > 0, mistake
+
+
+def test_unplanted_restatement_agrees(oracle_lib):
+    """The numpy restatement above, with no mistake planted, agrees with the golden vectors (so the mutants fail
+    only because of their mistake)."""
+    for name in ("cfg1_slice", "odd_tail"):
+        f = load_fixture(name)
+        y, sx = _mutant_linear(oracle_lib, f, None)
+        np.testing.assert_array_equal(sx, f["sx"])
+        np.testing.assert_array_equal(y, f["y"])
+
+
+# -------------------------------------------------------------------- checkpoint quantizer (test_int8.py:31-36)
+
+
+def test_quantize_weight_against_a_direct_float64_loop(oracle_lib):
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((6, 32)) * 0.02
+    q, ws = oracle_lib.quantize_weight(w, 16)
+    h = oracle_lib.regular_hadamard(16)
+    for o, k0 in itertools.product(range(6), range(0, 32, 16)):
+        for j in range(16):
+            rot = sum(w[o, k0 + i] * h[i, j] for i in range(16))
+            amax = max(abs(sum(w[o, kk0 + i] * h[i, jj] for i in range(16)))
+                       for kk0 in range(0, 32, 16) for jj in range(16))
+            assert abs(float(ws[o]) - amax / 127.0) <= 1e-7 * amax
+            assert int(q[o, k0 + j]) == int(np.clip(np.round(rot / (amax / 127.0)), -127, 127))
