@@ -150,8 +150,8 @@ __global__ __launch_bounds__(256) void rotate_quant_kernel(const uint16_t* __res
 
     amax = wave_max(amax);
     // amax of xr = amax of the unnormalised sums * 2^-n (exact); then the reference's clamp and division.
-    const float sx = fmaxf(ldexpf(amax, -2 * LOG4G), 1e-12f) / 127.0f;
-    const float d = ldexpf(sx, 2 * LOG4G);  // (t * 2^n) / (sx * 2^n) == xr / sx exactly
+    const float sx = fmaxf(ldexpf(amax, -LOG4G), 1e-12f) / 127.0f;
+    const float d = ldexpf(sx, LOG4G);  // (t * 2^n) / (sx * 2^n) == xr / sx exactly
     if (lane == 0) s[row] = sx;
     wave_lds_sync();
 
