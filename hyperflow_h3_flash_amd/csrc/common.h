@@ -24,6 +24,13 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
   return ((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : r;
 }
 
+// Two fp32 -> packed bf16 pair (lo, hi) with gfx950's v_cvt_pk_bf16_f32: round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
+}
+
 // Rounds an fp64 value to 8 significant bits (bf16 precision) with round-to-nearest-even, once, directly from the
 // fp64 bits: the kept bits end at bit 13 of the high word; bit 12 is the rounding bit and bits 11..0 of the high
 // word plus the whole low word are sticky. Adding 0xFFF + (lsb | sticky_low) carries into bit 13 exactly when RNE

@@ -62,9 +62,9 @@ int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream) {
   if (tiles == 0) return HF_OK;
   if (tiles >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   if (i32) {
-    hipLaunchKernelGGL(hf::int8_gemm_kernel<true>, dim3((unsigned)tiles), dim3(256), hf::kGemmLds, stream, a);
+    hipLaunchKernelGGL(hf::int8_gemm_kernel<true>, dim3((unsigned)tiles), dim3(hf::kThreads), hf::kGemmLds, stream, a);
   } else {
-    hipLaunchKernelGGL(hf::int8_gemm_kernel<false>, dim3((unsigned)tiles), dim3(256), hf::kGemmLds, stream, a);
+    hipLaunchKernelGGL(hf::int8_gemm_kernel<false>, dim3((unsigned)tiles), dim3(hf::kThreads), hf::kGemmLds, stream, a);
   }
   return launch_status();
 }
@@ -156,6 +156,7 @@ int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, c
   a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.sx = sx; a.sw = sw;
   a.u = r > 0 ? u : nullptr; a.ldu = ldu; a.up = r > 0 ? up : nullptr; a.ldup = ld_up; a.r = r;
   a.bias = bias; a.out = y; a.ldo = ldy; a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  a.out_vec16 = aligned(y, 16) && (ldy % 8) == 0;
   return launch_gemm(a, false, static_cast<hipStream_t>(stream));
 }
 

@@ -8,22 +8,34 @@
 //   y[m, n]   = bf16((f32(acc) * sx[m]) * sw[n] + sum_j u[m, j] * up[n, j] + bias[n])
 // With no low-rank branch and no bias the output is bitwise the reference's.
 //
-// Tiling: 256 (m) x 256 (n) output tile per workgroup, K in steps of 128 bytes, 4 waves in a 2 x 2 grid, each wave
-// a 128 x 128 sub-tile of 4 x 4 v_mfma_i32_32x32x32_i8 blocks. The MFMA's first operand is the weight (its rows
-// are the output columns n) and the second the activation, so each lane ends with four consecutive n of one row m:
-// the epilogue stores 8 contiguous bytes per lane and reads one activation scale per block.
+// Tiling: 256 (m) x 256 (n) output tile per workgroup (one per CU), K in stages of 64 bytes, 8 waves (two per SIMD,
+// so one wave's barrier wait and load issue run under the other's MFMAs) in a 2 (m) x 4 (n) grid, each wave a
+// 128 x 64 sub-tile of 4 x 2 v_mfma_i32_32x32x32_i8 blocks (128 accumulator registers). The
+// MFMA's first operand is the weight (its rows are the output columns n) and the second the activation, so each
+// lane ends with four consecutive n of one row m and reads one activation scale per block.
 //
-// Operands go global -> LDS with buffer_load ... lds (16 bytes per lane, no VGPR round trip), double-buffered.
-// A 128-byte LDS row holds one tile row's 128 K-bytes as eight 16-byte chunks, chunk c stored at c ^ (row & 7), so
-// the 32 rows one ds_read_b128 touches spread over all banks. Out-of-range rows and K beyond the end read as zero
-// through the buffer descriptor's range check.
+// Operands go global -> LDS with buffer_load ... lds (16 bytes per lane, no VGPR round trip) into a 4-stage ring
+// (128 KiB); the waits are partial (vmcnt counts the loads still allowed in flight) and the barrier carries no
+// memory fence, so three stages stay in flight while one is consumed. MFMA operands are double-buffered in
+// registers: the LDS reads of one 32-byte K step overlap the MFMAs of the previous one. Out-of-range rows and K
+// beyond the end read as zero through the buffer descriptor's range check. The epilogue goes through LDS so the
+// output is written as whole 128-byte row segments, 16 bytes per lane.
 #include "common.h"
 
 namespace hf {
 
-constexpr int GBM = 256, GBN = 256, GBK = 128;
-constexpr int kStageBytes = (GBM + GBN) * GBK;  // 64 KiB: activation tile then weight tile
-constexpr int kGemmLds = 2 * kStageBytes;       // double buffered
+constexpr int GBM = 256;                          // activation rows (m) per workgroup tile
+constexpr int GBN = 256;                          // weight rows (n) per workgroup tile
+constexpr int GBK = 64;                           // K bytes per pipeline stage
+constexpr int kStages = 4;                        // LDS ring depth
+constexpr int kAStage = GBM * GBK;                // 16 KiB
+constexpr int kBStage = GBN * GBK;                // 16 KiB
+constexpr int kStageBytes = kAStage + kBStage;    // 32 KiB
+constexpr int kRingBytes = kStages * kStageBytes; // 128 KiB; the epilogue reuses it as a 256 x 256 bf16 tile
+constexpr int kParamBytes = 3 * 256 * 4;          // the tile's sx, wscale and bias (fp32), staged at kernel start
+constexpr int kGemmLds = kRingBytes + kParamBytes;
+constexpr int kWaves = 8;                         // 2 per SIMD: one wave's barrier and load issue hide under the other's MFMAs
+constexpr int kThreads = 64 * kWaves;
 
 struct GemmArgs {
   const int8_t* q;
@@ -42,46 +54,91 @@ struct GemmArgs {
   int64_t ldo;
   int M, N, K;
   int tiles_m, tiles_n;
+  int out_vec16;         // bf16 rows may be written 16 bytes at a time (16-byte aligned base and ldo % 8 == 0)
 };
 
-// Workgroup id -> (tile_m, tile_n). Workgroups are dealt to the 8 XCDs round robin; renumber them so each XCD gets
-// a contiguous run of tiles, then walk that run in groups of 8 tile rows so tiles sharing weight columns (and
-// activation rows) run close together on one XCD's L2.
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int total = tiles_m * tiles_n;
-  const int per = total / 8, rem = total % 8;
-  const int xcd = bid % 8, local = bid / 8;
-  const int logical = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-  constexpr int kGroupM = 8;
-  const int group = kGroupM * tiles_n;
-  const int first_m = (logical / group) * kGroupM;
-  const int size_m = min(tiles_m - first_m, kGroupM);
-  tm = first_m + (logical % group) % size_m;
-  tn = (logical % group) / size_m;
+// Workgroup id -> (tile_m, tile_n), row-major: consecutive workgroups share an activation row block and are dealt
+// round robin to the 8 XCDs, so each XCD's L2 sees a quarter of the weight column blocks per row (measured faster
+// than grouping each XCD's tiles into a contiguous block).
+__device__ __forceinline__ void tile_of(int bid, int tiles_n, int& tm, int& tn) {
+  tm = bid / tiles_n;
+  tn = bid % tiles_n;
 }
 
-__device__ __forceinline__ void load_tile_rows(__amdgpu_buffer_rsrc_t rsrc, uint32_t oob, int64_t ld, int rows_valid,
-                                               int k0, int K, unsigned char HF_LDS* dst, int wave, int lane) {
-  // 256 rows x 128 bytes = 32 loads of 1 KiB (8 rows) per tile; 8 per wave.
+// LDS rows are 64 bytes (four 16-byte chunks of K); chunk c of row r lives at c ^ ((r >> 1) & 3), which spreads the
+// 32 rows of one fragment read over all banks (measured conflict-free on gfx950 for ds_read_b128).
+__device__ __forceinline__ int swizzle(int r, int c) { return c ^ ((r >> 1) & 3); }
+
+// Per-lane byte offsets of one wave's stage loads, computed once per tile. Load i of a wave fills LDS block
+// blk = first_blk + i (16 rows x 64 bytes): lane l fills row 16*blk + l/4, physical chunk l%4, from the logical chunk
+// the swizzle stores there. Rows past the tile's valid rows get the descriptor size as base offset, so adding any
+// K offset keeps them out of range (they read as zero).
+template <int COUNT>
+struct StageOffsets {
+  uint32_t off[COUNT];
+  __device__ __forceinline__ void init(uint32_t oob, int64_t ld, int rows_valid, int first_blk, int lane) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int blk = wave * 8 + i;
-    const int r = blk * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ (r & 7);
-    const int kb = k0 + c * 16;
-    const uint32_t voff = (r < rows_valid && kb < K) ? (uint32_t)(r * ld + kb) : oob;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + blk * 1024), 16, voff, 0, 0, 0);
+    for (int i = 0; i < COUNT; ++i) {
+      const int r = (first_blk + i) * 16 + (lane >> 2);
+      const int c = swizzle(r, lane & 3);
+      off[i] = r < rows_valid ? (uint32_t)(r * ld + c * 16) : oob;
+    }
+  }
+};
+
+// Issue one wave's loads of a stage at K offset k0 into `dst` (LDS, wave-uniform). Chunks at or past K (only in a
+// partial last stage) read as zero; so does every load of a stage past the end (k0 >= K).
+template <int COUNT>
+__device__ __forceinline__ void load_stage(__amdgpu_buffer_rsrc_t rsrc, const StageOffsets<COUNT>& so, uint32_t oob,
+                                           int k0, int K, unsigned char HF_LDS* dst, int first_blk, int lane) {
+  const bool partial = k0 + GBK > K;
+#pragma unroll
+  for (int i = 0; i < COUNT; ++i) {
+    uint32_t voff = so.off[i] + (uint32_t)k0;
+    if (partial) {
+      const int kb = k0 + swizzle((first_blk + i) * 16 + (lane >> 2), lane & 3) * 16;
+      if (kb >= K) voff = oob;
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + (first_blk + i) * 1024), 16, voff, 0, 0, 0);
   }
 }
 
+struct Frags {
+  v4i a[4];  // activation rows: 4 blocks of 32 (the wave's 128 m)
+  v4i b[2];  // weight rows: 2 blocks of 32 (the wave's 64 n)
+};
+
+__device__ __forceinline__ void read_frags(Frags& f, const unsigned char HF_LDS* stage, int wm, int wn, int ks,
+                                           int sub, int half) {
+  const int chunk = swizzle(sub, 2 * ks + half) * 16;  // (row >> 1) & 3 == (sub >> 1) & 3: blocks start at 32k
+  const unsigned char HF_LDS* As = stage;
+  const unsigned char HF_LDS* Bs = stage + kAStage;
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) f.a[jb] = *(const v4i HF_LDS*)(As + (wm * 128 + jb * 32 + sub) * GBK + chunk);
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib) f.b[ib] = *(const v4i HF_LDS*)(Bs + (wn * 64 + ib * 32 + sub) * GBK + chunk);
+}
+
+__device__ __forceinline__ void mma(v16i (&acc)[2][4], const Frags& f) {
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+      acc[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[ib], f.a[jb], acc[ib][jb], 0, 0, 0);
+}
+
+#define HF_BARRIER() asm volatile("s_barrier" ::: "memory")
+
 template <bool I32OUT>
-__global__ __launch_bounds__(256, 1) void int8_gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[];
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)smem_raw;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps LDS addresses scalar
+  const int wm = wave & 1, wn = wave >> 1;  // 2 (m) x 4 (n) waves of 128 x 64
+  const int sub = lane & 31, half = lane >> 5;
   int tm, tn;
-  tile_of(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
+  tile_of(blockIdx.x, a.tiles_n, tm, tn);
   const int m0 = tm * GBM, n0 = tn * GBN;
   const int rows_m = min(GBM, a.M - m0), rows_n = min(GBN, a.N - n0);
 
@@ -89,44 +146,93 @@ __global__ __launch_bounds__(256, 1) void int8_gemm_kernel(GemmArgs a) {
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q + (int64_t)m0 * a.ldq, bytes_q);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + (int64_t)n0 * a.ldw, bytes_w);
 
-  v16i acc[4][4];
+  StageOffsets<2> offq, offw;
+  offq.init(bytes_q, a.ldq, rows_m, wave * 2, lane);
+  offw.init(bytes_w, a.ldw, rows_n, wave * 2, lane);
+  // Stage kt into slot kt % 4; a stage past the end (kt >= nk) loads zeros, which keeps the loop branch-free.
+  auto issue_stage = [&](int kt) {
+    unsigned char HF_LDS* st = smem + (kt % kStages) * kStageBytes;
+    load_stage<2>(rq, offq, bytes_q, kt * GBK, a.K, st, wave * 2, lane);
+    load_stage<2>(rw, offw, bytes_w, kt * GBK, a.K, st + kAStage, wave * 2, lane);
+  };
+
+  // The epilogue's per-row and per-column factors, loaded into registers now and parked in LDS beside the ring when
+  // the epilogue starts, so no epilogue instruction waits on global memory. Threads 0..255 take row m0 + t and
+  // column n0 + t (sx, wscale); threads 256..511 take the bias of column n0 + t - 256.
+  float HF_LDS* params = (float HF_LDS*)(smem + kRingBytes);
+  float p_val = 0.0f;
+  uint32_t p_bias = 0;
+  const int pt = threadIdx.x & 255;
+  if (!I32OUT) {
+    // Branch-free (clamped indices, a stand-in array when there is no bias) so no wait lands here; rows and columns
+    // past the edge are masked when the values are parked.
+    if (threadIdx.x < 256) {
+      p_val = a.sx[min(m0 + pt, a.M - 1)];
+      p_bias = __float_as_uint(a.sw[min(n0 + pt, a.N - 1)]);
+    } else {
+      const uint16_t* bsrc = a.bias ? a.bias : reinterpret_cast<const uint16_t*>(a.sw);
+      p_bias = bsrc[min(n0 + pt, a.N - 1)];
+    }
+  }
+
+  v16i acc[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (v16i){0};
 
   const int nk = (a.K + GBK - 1) / GBK;
-  load_tile_rows(rq, bytes_q, a.ldq, rows_m, 0, a.K, smem, wave, lane);
-  load_tile_rows(rw, bytes_w, a.ldw, rows_n, 0, a.K, smem + GBM * GBK, wave, lane);
+  // Prologue: stages 0..3 in flight (4 loads per wave per stage), wait for stage 0.
+  issue_stage(0);
+  issue_stage(1);
+  issue_stage(2);
+  issue_stage(3);
+  asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  HF_BARRIER();
+  Frags f0, f1;
+  read_frags(f0, smem, wm, wn, 0, sub, half);
 
-  const int sub = lane & 31, half = lane >> 5;
+  // Stage kt lives in slot kt % 4. Per stage: read the second K half while multiplying the first; wait for this
+  // wave's loads of stage kt+1 (stages kt+2 and kt+3 stay in flight) and for the reads of slot kt % 4; barrier;
+  // read stage kt+1's first half, refill slot kt % 4 with stage kt+4 and multiply the second half, with the LDS
+  // reads and loads spread between the MFMAs. Past the last stage the reads and loads are harmless (in-bounds
+  // slots, zero-filled loads), so the body has no branches.
   for (int kt = 0; kt < nk; ++kt) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (kt + 1 < nk) {
-      unsigned char HF_LDS* nxt = smem + ((kt + 1) & 1) * kStageBytes;
-      load_tile_rows(rq, bytes_q, a.ldq, rows_m, (kt + 1) * GBK, a.K, nxt, wave, lane);
-      load_tile_rows(rw, bytes_w, a.ldw, rows_n, (kt + 1) * GBK, a.K, nxt + GBM * GBK, wave, lane);
-    }
-    const unsigned char HF_LDS* As = smem + (kt & 1) * kStageBytes;
-    const unsigned char HF_LDS* Bs = As + GBM * GBK;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int chunk = ((2 * ks + half) ^ (sub & 7)) * 16;
-      v4i wf[4], af[4];
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
-        wf[ib] = *(const v4i HF_LDS*)(Bs + (wn * 128 + ib * 32 + sub) * GBK + chunk);
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
-        af[jb] = *(const v4i HF_LDS*)(As + (wm * 128 + jb * 32 + sub) * GBK + chunk);
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-          acc[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[ib], af[jb], acc[ib][jb], 0, 0, 0);
-    }
+    const unsigned char HF_LDS* st = smem + (kt % kStages) * kStageBytes;
+    read_frags(f1, st, wm, wn, 1, sub, half);
+    mma(acc, f0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
+    __builtin_amdgcn_sched_barrier(0);  // every MFMA of the first half issues before the wait and barrier
+    asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+    HF_BARRIER();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(f0, smem + ((kt + 1) % kStages) * kStageBytes, wm, wn, 0, sub, half);
+    issue_stage(kt + 4);
+    mma(acc, f1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // VMEM (stage load)
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  // Zero-fill loads past the end may still be landing in the ring; the epilogue reuses it.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Output layout of a 32x32 block: lane holds column j = lane % 32 (the row m here) and, in register v, row
   // i = 8*(v/4) + 4*(lane/32) + v%4 (the column n here): four consecutive n per group of four registers.
@@ -137,10 +243,10 @@ __global__ __launch_bounds__(256, 1) void int8_gemm_kernel(GemmArgs a) {
       const int m = m0 + wm * 128 + jb * 32 + sub;
       if (m >= a.M) continue;
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
+      for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = n0 + wn * 128 + ib * 32 + 8 * g + 4 * half;
+          const int n = n0 + wn * 64 + ib * 32 + 8 * g + 4 * half;
           int32_t* dst = out + (int64_t)m * a.ldo + n;
           const v16i& c = acc[ib][jb];
           if (n + 3 < a.N && ((a.ldo & 3) == 0)) {
@@ -152,25 +258,31 @@ __global__ __launch_bounds__(256, 1) void int8_gemm_kernel(GemmArgs a) {
         }
     }
   } else {
-    // One 32-wide block of output columns at a time keeps a single 64-register fp32 tile live next to the
-    // accumulators: dequantize, add the low-rank product on bf16 MFMA, add the bias, round, store.
+    // Dequantize one 32-wide block of output columns at a time (add the low-rank product on bf16 MFMA and the
+    // bias), round to bf16 and park it in LDS as this wave's 128 x 64 tile (rows of 128 bytes, 16-byte chunk c of
+    // row r at c ^ (r & 7)); then write whole 128-byte row segments, 16 bytes per lane, 8 rows per instruction.
+    if (threadIdx.x < 256) {
+      params[pt] = (m0 + pt < a.M) ? p_val : 0.0f;
+      params[256 + pt] = (n0 + pt < a.N) ? __uint_as_float(p_bias) : 0.0f;
+    } else {
+      params[512 + pt] = (n0 + pt < a.N && a.bias) ? __uint_as_float(p_bias << 16) : 0.0f;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    HF_BARRIER();
     float sxv[4];
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      const int m = m0 + wm * 128 + jb * 32 + sub;
-      sxv[jb] = m < a.M ? a.sx[m] : 0.0f;
-    }
-    uint16_t* out = static_cast<uint16_t*>(a.out);
-    const bool vec = (a.ldo & 3) == 0;
+    for (int jb = 0; jb < 4; ++jb) sxv[jb] = params[wm * 128 + jb * 32 + sub];
+    unsigned char HF_LDS* tile = smem + wave * (128 * 128);
+    const bool has_bias = a.bias != nullptr;
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      const int nb = n0 + wn * 128 + ib * 32;
+    for (int ib = 0; ib < 2; ++ib) {
+      const int nb = n0 + wn * 64 + ib * 32;
       float ws[16], bv[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int n = nb + 8 * (v >> 2) + 4 * half + (v & 3);
-        ws[v] = n < a.N ? a.sw[n] : 0.0f;
-        bv[v] = (a.bias && n < a.N) ? __uint_as_float((uint32_t)a.bias[n] << 16) : 0.0f;
+        const int nl = wn * 64 + ib * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+        ws[v] = params[256 + nl];
+        bv[v] = params[512 + nl];
       }
       v16f c[4];
 #pragma unroll
@@ -196,26 +308,39 @@ __global__ __launch_bounds__(256, 1) void int8_gemm_kernel(GemmArgs a) {
       }
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
-        const int m = m0 + wm * 128 + jb * 32 + sub;
-        if (m >= a.M) continue;
+        const int r = jb * 32 + sub;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = nb + 8 * g + 4 * half;
-          uint32_t h[4];
+          float v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            float v = c[jb][4 * g + e];
-            if (a.bias) v = v + bv[4 * g + e];
-            h[e] = f32_to_bf16_rne(v);
+            v[e] = c[jb][4 * g + e];
+            if (has_bias) v[e] = v[e] + bv[4 * g + e];
           }
-          uint16_t* dst = out + (int64_t)m * a.ldo + n;
-          if (vec && n + 3 < a.N) {
-            *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-          } else {
-            for (int e = 0; e < 4; ++e)
-              if (n + e < a.N) dst[e] = (uint16_t)h[e];
-          }
+          const int chunk = (4 * ib + g) ^ (r & 7);
+          typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+          *(v2u HF_LDS*)(tile + r * 128 + chunk * 16 + 8 * half) = (v2u){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
+      }
+    }
+    wave_lds_sync();
+    uint16_t* out = static_cast<uint16_t*>(a.out);
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+      const int r = i * 8 + (lane >> 3);
+      const int p = lane & 7;
+      const int c = p ^ (r & 7);
+      const v4i v = *(const v4i HF_LDS*)(tile + r * 128 + p * 16);
+      const int m = m0 + wm * 128 + r;
+      const int n = n0 + wn * 64 + c * 8;
+      if (m >= a.M) continue;
+      uint16_t* dst = out + (int64_t)m * a.ldo + n;
+      if (a.out_vec16 && n + 7 < a.N) {
+        *reinterpret_cast<v4i*>(dst) = v;
+      } else {
+        const uint32_t wds[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+        for (int e = 0; e < 8; ++e)
+          if (n + e < a.N) dst[e] = (uint16_t)(wds[e >> 1] >> (16 * (e & 1)));
       }
     }
   }

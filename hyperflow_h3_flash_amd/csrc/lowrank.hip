@@ -35,7 +35,6 @@ __global__ __launch_bounds__(256) void lowrank_down_kernel(const uint16_t* __res
 
   // K is a multiple of 16; wave w takes the 16-element steps w, w + 4, w + 8, ...
   const int steps = K / 16;
-#pragma unroll 2
   for (int st = wave; st < steps; st += 4) {
     const int k = st * 16 + 8 * half;
     const v8bf xf = *reinterpret_cast<const v8bf*>(xrow + k);
