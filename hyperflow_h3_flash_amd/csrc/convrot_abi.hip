@@ -122,7 +122,7 @@ int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_
     return HF_ERR_ALIGNMENT;
   if (M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned blocks = (unsigned)((M + 31) / 32);
+  const unsigned blocks = (unsigned)((M + hf::kLrRows - 1) / hf::kLrRows);
   for (int32_t j0 = 0; j0 < r; j0 += 128) {
     const int rr = std::min<int32_t>(128, r - j0);
     const uint16_t* d = down + (int64_t)j0 * ld_down;
@@ -151,6 +151,7 @@ int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, c
   if (r > 0) {
     if (!u || !up || ldu < r || ld_up < r) return HF_ERR_ARGUMENT;
     if ((r % 8) || !aligned(u, 16) || !aligned(up, 16) || (ldu % 8) || (ld_up % 8)) return HF_ERR_ALIGNMENT;
+    if (512 * ldu >= (int64_t(1) << 31) || 512 * ld_up >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   }
   hf::GemmArgs a{};
   a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.sx = sx; a.sw = sw;

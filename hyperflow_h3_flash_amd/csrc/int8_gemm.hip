@@ -18,8 +18,9 @@
 // (128 KiB); the waits are partial (vmcnt counts the loads still allowed in flight) and the barrier carries no
 // memory fence, so three stages stay in flight while one is consumed. MFMA operands are double-buffered in
 // registers: the LDS reads of one 32-byte K step overlap the MFMAs of the previous one. Out-of-range rows and K
-// beyond the end read as zero through the buffer descriptor's range check. The epilogue goes through LDS so the
-// output is written as whole 128-byte row segments, 16 bytes per lane.
+// beyond the end read as zero through the buffer descriptor's range check. A rank <= 64 low-rank branch rides the
+// last two refills into the ring, so the epilogue reads its operands from LDS. The epilogue goes through LDS so the
+// output is written as whole 64-byte row segments, 16 bytes per lane.
 #include "common.h"
 
 namespace hf {
@@ -100,6 +101,22 @@ __device__ __forceinline__ void load_stage(__amdgpu_buffer_rsrc_t rsrc, const St
       if (kb >= K) voff = oob;
     }
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + (first_blk + i) * 1024), 16, voff, 0, 0, 0);
+  }
+}
+
+// The low-rank operands of a tile (u rows m or up rows n, rank r <= 64, as 128-byte rows of 8 chunks of 8 bf16,
+// chunk c of row i stored at c ^ (i & 7)) are loaded into a free ring slot: 256 rows x 128 bytes = 32 loads of
+// 1 KiB, 4 per wave. Rows past the tile's valid rows and chunks past r read as zero.
+__device__ __forceinline__ void load_lowrank_rows(__amdgpu_buffer_rsrc_t rsrc, uint32_t oob, int64_t ld_bytes,
+                                                  int rows_valid, int r, unsigned char HF_LDS* dst, int wave,
+                                                  int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int blk = wave * 4 + i;
+    const int row = blk * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ (row & 7);
+    const uint32_t voff = (row < rows_valid && c * 8 < r) ? (uint32_t)(row * ld_bytes + c * 16) : oob;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + blk * 1024), 16, voff, 0, 0, 0);
   }
 }
 
@@ -192,12 +209,23 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   Frags f0, f1;
   read_frags(f0, smem, wm, wn, 0, sub, half);
 
+  // With a rank <= 64 low-rank branch, the u tile [256 m][r] and the up tile [256 n][r] take the places of the
+  // stage loads the last iterations would not need; they land in the ring slots nk % 4 and (nk + 1) % 4.
+  const bool lr_lds = !I32OUT && a.r > 0 && a.r <= 64 && nk >= kStages;
+  __amdgpu_buffer_rsrc_t ru = rq, rup = rw;
+  uint32_t bytes_u = 0, bytes_up = 0;
+  if (lr_lds) {
+    bytes_u = (uint32_t)(rows_m * a.ldu * 2);
+    bytes_up = (uint32_t)(rows_n * a.ldup * 2);
+    ru = make_rsrc(a.u + (int64_t)m0 * a.ldu, bytes_u);
+    rup = make_rsrc(a.up + (int64_t)n0 * a.ldup, bytes_up);
+  }
+
   // Stage kt lives in slot kt % 4. Per stage: read the second K half while multiplying the first; wait for this
-  // wave's loads of stage kt+1 (stages kt+2 and kt+3 stay in flight) and for the reads of slot kt % 4; barrier;
-  // read stage kt+1's first half, refill slot kt % 4 with stage kt+4 and multiply the second half, with the LDS
-  // reads and loads spread between the MFMAs. Past the last stage the reads and loads are harmless (in-bounds
-  // slots, zero-filled loads), so the body has no branches.
-  for (int kt = 0; kt < nk; ++kt) {
+  // wave's loads of stage kt+1 (two more stages stay in flight) and for the reads of slot kt % 4; barrier; read
+  // stage kt+1's first half, refill slot kt % 4 and multiply the second half, with the LDS reads and loads spread
+  // between the MFMAs. Skipping a refill (the tail) only makes the partial wait stricter, never looser.
+  auto stage_body = [&](int kt, int refill) {
     const unsigned char HF_LDS* st = smem + (kt % kStages) * kStageBytes;
     read_frags(f1, st, wm, wn, 1, sub, half);
     mma(acc, f0);
@@ -213,7 +241,15 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     HF_BARRIER();
     __builtin_amdgcn_sched_barrier(0);
     read_frags(f0, smem + ((kt + 1) % kStages) * kStageBytes, wm, wn, 0, sub, half);
-    issue_stage(kt + 4);
+    unsigned char HF_LDS* slot = smem + (kt % kStages) * kStageBytes;
+    if (refill == 0) {
+      load_stage<2>(rq, offq, bytes_q, (kt + 4) * GBK, a.K, slot, wave * 2, lane);
+      load_stage<2>(rw, offw, bytes_w, (kt + 4) * GBK, a.K, slot + kAStage, wave * 2, lane);
+    } else if (refill == 1) {
+      load_lowrank_rows(ru, bytes_u, a.ldu * 2, rows_m, a.r, slot, wave, lane);
+    } else if (refill == 2) {
+      load_lowrank_rows(rup, bytes_up, a.ldup * 2, rows_n, a.r, slot, wave, lane);
+    }
     mma(acc, f1);
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
@@ -230,6 +266,15 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     __builtin_amdgcn_sched_barrier(0);
+  };
+  const int steady = nk - kStages;  // iterations whose refill is a real stage
+  int kt = 0;
+  for (; kt < steady; ++kt) stage_body(kt, 0);
+  for (; kt < nk; ++kt) {
+    int refill = 3;  // nothing: the stages a short K needs were issued up front
+    if (lr_lds && kt == steady) refill = 1;
+    if (lr_lds && kt == steady + 1) refill = 2;
+    stage_body(kt, refill);
   }
   // Zero-fill loads past the end may still be landing in the ring; the epilogue reuses it.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -259,8 +304,10 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     }
   } else {
     // Dequantize one 32-wide block of output columns at a time (add the low-rank product on bf16 MFMA and the
-    // bias), round to bf16 and park it in LDS as this wave's 128 x 64 tile (rows of 128 bytes, 16-byte chunk c of
-    // row r at c ^ (r & 7)); then write whole 128-byte row segments, 16 bytes per lane, 8 rows per instruction.
+    // bias), round to bf16 and park it in LDS (this wave's 128 x 32 block: rows of 64 bytes, 16-byte chunk c of row
+    // i at c ^ ((i >> 1) & 3)), then write 64-byte row segments, 16 bytes per lane, 16 rows per instruction. The
+    // staging uses the two ring slots the low-rank tiles do not: waves 0-3 slot (nk + 2) % 4, waves 4-7 slot
+    // (nk + 3) % 4, 8 KiB each.
     if (threadIdx.x < 256) {
       params[pt] = (m0 + pt < a.M) ? p_val : 0.0f;
       params[256 + pt] = (n0 + pt < a.N) ? __uint_as_float(p_bias) : 0.0f;
@@ -272,8 +319,12 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     float sxv[4];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) sxv[jb] = params[wm * 128 + jb * 32 + sub];
-    unsigned char HF_LDS* tile = smem + wave * (128 * 128);
+    const unsigned char HF_LDS* u_lds = smem + (nk % kStages) * kStageBytes;
+    const unsigned char HF_LDS* up_lds = smem + ((nk + 1) % kStages) * kStageBytes;
+    unsigned char HF_LDS* tile =
+        smem + ((nk + 2 + (wave >> 2)) % kStages) * kStageBytes + (wave & 3) * (128 * 64);
     const bool has_bias = a.bias != nullptr;
+    uint16_t* out = static_cast<uint16_t*>(a.out);
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib) {
       const int nb = n0 + wn * 64 + ib * 32;
@@ -292,8 +343,21 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
           const float t = (float)acc[ib][jb][v] * sxv[jb];
           c[jb][v] = t * ws[v];
         }
-      if (a.r > 0) {
-        // Low-rank term on bf16 MFMA into the same fp32 tile: first operand up[n, :], second u[m, :].
+      if (lr_lds) {
+        // Low-rank term from the LDS tiles: first operand up[n, :], second u[m, :], 16 ranks per MFMA.
+        const int nl = wn * 64 + ib * 32 + sub;
+        for (int kk = 0; kk < a.r; kk += 16) {
+          const int chunk = kk / 8 + half;
+          const v8bf pf = *(const v8bf HF_LDS*)(up_lds + nl * 128 + ((chunk ^ (nl & 7)) * 16));
+#pragma unroll
+          for (int jb = 0; jb < 4; ++jb) {
+            const int ml = wm * 128 + jb * 32 + sub;
+            const v8bf uf = *(const v8bf HF_LDS*)(u_lds + ml * 128 + ((chunk ^ (ml & 7)) * 16));
+            c[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[jb], 0, 0, 0);
+          }
+        }
+      } else if (a.r > 0) {
+        // Ranks above 64 (or a K too short to carry them in the ring): the same product from global memory.
         const int nrow = min(nb + sub, a.N - 1);
         for (int kk = 0; kk < a.r; kk += 16) {
           const int k = kk + 8 * half;
@@ -308,7 +372,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       }
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
-        const int r = jb * 32 + sub;
+        const int rr = jb * 32 + sub;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           float v[4];
@@ -317,31 +381,32 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
             v[e] = c[jb][4 * g + e];
             if (has_bias) v[e] = v[e] + bv[4 * g + e];
           }
-          const int chunk = (4 * ib + g) ^ (r & 7);
+          const int chunk = g ^ ((rr >> 1) & 3);
           typedef unsigned int v2u __attribute__((ext_vector_type(2)));
-          *(v2u HF_LDS*)(tile + r * 128 + chunk * 16 + 8 * half) = (v2u){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          *(v2u HF_LDS*)(tile + rr * 64 + chunk * 16 + 8 * half) = (v2u){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
       }
-    }
-    wave_lds_sync();
-    uint16_t* out = static_cast<uint16_t*>(a.out);
-#pragma unroll 4
-    for (int i = 0; i < 16; ++i) {
-      const int r = i * 8 + (lane >> 3);
-      const int p = lane & 7;
-      const int c = p ^ (r & 7);
-      const v4i v = *(const v4i HF_LDS*)(tile + r * 128 + p * 16);
-      const int m = m0 + wm * 128 + r;
-      const int n = n0 + wn * 64 + c * 8;
-      if (m >= a.M) continue;
-      uint16_t* dst = out + (int64_t)m * a.ldo + n;
-      if (a.out_vec16 && n + 7 < a.N) {
-        *reinterpret_cast<v4i*>(dst) = v;
-      } else {
-        const uint32_t wds[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
-        for (int e = 0; e < 8; ++e)
-          if (n + e < a.N) dst[e] = (uint16_t)(wds[e >> 1] >> (16 * (e & 1)));
+      wave_lds_sync();
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int rr = i * 16 + (lane >> 2);
+        const int p = lane & 3;
+        const int cc = p ^ ((rr >> 1) & 3);
+        const v4i v = *(const v4i HF_LDS*)(tile + rr * 64 + p * 16);
+        const int m = m0 + wm * 128 + rr;
+        const int n = nb + cc * 8;
+        if (m < a.M) {
+          uint16_t* dst = out + (int64_t)m * a.ldo + n;
+          if (a.out_vec16 && n + 7 < a.N) {
+            *reinterpret_cast<v4i*>(dst) = v;
+          } else {
+            const uint32_t wds[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+            for (int e = 0; e < 8; ++e)
+              if (n + e < a.N) dst[e] = (uint16_t)(wds[e >> 1] >> (16 * (e & 1)));
+          }
+        }
       }
+      wave_lds_sync();  // the block is overwritten by the next one
     }
   }
 }

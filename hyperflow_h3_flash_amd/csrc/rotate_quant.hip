@@ -4,7 +4,7 @@
 // arithmetic of its torch path (int8.py:176-178):
 //   xr = bf16(x @ blockdiag(R))   R = regular Hadamard of order G = 4^n, entries +-2^-n
 //   sx = max(absmax_row(xr), 1e-12) / 127          (fp32, correctly rounded division)
-//   xq = clamp(rint(xr / sx), -127, 127)           (fp32, correctly rounded division, ties to even)
+//   xq = clamp(rint(xr / sx), -127, 127)           (fp32, correctly rounded quotient, ties to even)
 //
 // The rotation is the unnormalised radix-4 butterfly H4 v = S - 2 reverse(v) (S = sum of the four), applied along
 // each base-4 digit of the in-group index, in fp64. Every product with +-1 and every partial sum is exact in fp64
@@ -40,6 +40,15 @@ __device__ __forceinline__ void h4_stage(double (&v)[16]) {
   for (int base = 0; base < 16; ++base) {
     if ((base / S) % 4 == 0) h4(v[base], v[base + S], v[base + 2 * S], v[base + 3 * S]);
   }
+}
+
+// RN(a / d) for a bf16-precision a (at most 8 significant bits) and inv = RN(1 / d), in three operations: the
+// remainder of q0 = RN(a * inv) is exact in one fma and one more fma corrects q0 (Markstein). Checked exhaustively
+// against the correctly rounded division for every fp32 significand of d (tests/proofs/markstein_quotient.c).
+__device__ __forceinline__ float quotient(float a, float d, float inv) {
+  const float q0 = a * inv;
+  const float r = fmaf(-q0, d, a);
+  return fmaf(r, inv, q0);
 }
 
 size_t rotate_quant_lds_bytes(int waves, int K) { return (size_t)waves * (kRqScratchBytes + 2 * (size_t)K); }
@@ -152,6 +161,7 @@ __global__ __launch_bounds__(256) void rotate_quant_kernel(const uint16_t* __res
     // amax of xr = amax of the unnormalised sums * 2^-n (exact); then the reference's clamp and division.
     const float sx = fmaxf(ldexpf(amax, -LOG4G), 1e-12f) / 127.0f;
     const float d = ldexpf(sx, LOG4G);  // (t * 2^n) / (sx * 2^n) == xr / sx exactly
+    const float inv = 1.0f / d;         // correctly rounded; the per-element quotients below use it
     if (lane == 0) s[row] = sx;
     wave_lds_sync();
 
@@ -169,8 +179,8 @@ __global__ __launch_bounds__(256) void rotate_quant_kernel(const uint16_t* __res
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const uint32_t pair = w[2 * i + h];
-          float r0 = rintf(bf16_lo(pair) / d);
-          float r1 = rintf(bf16_hi(pair) / d);
+          float r0 = rintf(quotient(bf16_lo(pair), d, inv));
+          float r1 = rintf(quotient(bf16_hi(pair), d, inv));
           r0 = fminf(fmaxf(r0, -127.0f), 127.0f);
           r1 = fminf(fmaxf(r1, -127.0f), 127.0f);
           word |= ((uint32_t)((int)r0 & 0xff) | ((uint32_t)((int)r1 & 0xff) << 8)) << (16 * h);

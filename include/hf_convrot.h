@@ -70,7 +70,7 @@ int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_
  * u: bf16 [M, ldu] or NULL; up: bf16 [N, ld_up] (LowRankLinear.up.weight) or NULL; r: rank (0 = none);
  * bias: bf16 [N] or NULL; y: bf16 [M, ldy].
  * Requires: K % 16 == 0; q, w 16-byte aligned; ldq, ldw multiples of 16; 256 * ldq and 256 * ldw < 2^31; y 8-byte aligned;
- * when r > 0: r % 8 == 0, u and up 16-byte aligned, ldu and ld_up multiples of 8.
+ * when r > 0: r % 8 == 0, u and up 16-byte aligned, ldu and ld_up multiples of 8, 512 * ldu and 512 * ld_up < 2^31.
  */
 int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
                    const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
