@@ -41,6 +41,10 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<4>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<1>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLrLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<2>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLrLds);
     (void)hipGetLastError();
   });
 }
@@ -121,18 +125,20 @@ int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_
   if (K % 16 || !aligned(x, 16) || !aligned(down, 16) || (ldx % 8) || (ld_down % 8) || !aligned(u, 8))
     return HF_ERR_ALIGNMENT;
   if (M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  if (2 * hf::kLrRows * ldx >= (int64_t(1) << 31) || 2 * hf::kLrRanks * ld_down >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  allow_large_lds();
   hipStream_t s = static_cast<hipStream_t>(stream);
   const unsigned blocks = (unsigned)((M + hf::kLrRows - 1) / hf::kLrRows);
-  for (int32_t j0 = 0; j0 < r; j0 += 128) {
-    const int rr = std::min<int32_t>(128, r - j0);
+  for (int32_t j0 = 0; j0 < r; j0 += hf::kLrRanks) {
+    const int rr = std::min<int32_t>(hf::kLrRanks, r - j0);
     const uint16_t* d = down + (int64_t)j0 * ld_down;
     uint16_t* uo = u + j0;
-    const int rb = (rr + 31) / 32;
-    switch (rb) {
-      case 1: hipLaunchKernelGGL(hf::lowrank_down_kernel<1>, dim3(blocks), dim3(256), 0, s, x, ldx, d, ld_down, uo, ldu, (int)M, (int)K, rr); break;
-      case 2: hipLaunchKernelGGL(hf::lowrank_down_kernel<2>, dim3(blocks), dim3(256), 0, s, x, ldx, d, ld_down, uo, ldu, (int)M, (int)K, rr); break;
-      case 3: hipLaunchKernelGGL(hf::lowrank_down_kernel<3>, dim3(blocks), dim3(256), 0, s, x, ldx, d, ld_down, uo, ldu, (int)M, (int)K, rr); break;
-      default: hipLaunchKernelGGL(hf::lowrank_down_kernel<4>, dim3(blocks), dim3(256), 0, s, x, ldx, d, ld_down, uo, ldu, (int)M, (int)K, rr); break;
+    if (rr <= 32) {
+      hipLaunchKernelGGL(hf::lowrank_down_kernel<1>, dim3(blocks), dim3(hf::kLrThreads), hf::kLrLds, s, x, ldx, d,
+                         ld_down, uo, ldu, (int)M, (int)K, rr);
+    } else {
+      hipLaunchKernelGGL(hf::lowrank_down_kernel<2>, dim3(blocks), dim3(hf::kLrThreads), hf::kLrLds, s, x, ldx, d,
+                         ld_down, uo, ldu, (int)M, (int)K, rr);
     }
     const int st = launch_status();
     if (st != HF_OK) return st;

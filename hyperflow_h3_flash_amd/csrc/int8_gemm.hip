@@ -58,12 +58,20 @@ struct GemmArgs {
   int out_vec16;         // bf16 rows may be written 16 bytes at a time (16-byte aligned base and ldo % 8 == 0)
 };
 
-// Workgroup id -> (tile_m, tile_n), row-major: consecutive workgroups share an activation row block and are dealt
-// round robin to the 8 XCDs, so each XCD's L2 sees a quarter of the weight column blocks per row (measured faster
-// than grouping each XCD's tiles into a contiguous block).
-__device__ __forceinline__ void tile_of(int bid, int tiles_n, int& tm, int& tn) {
-  tm = bid / tiles_n;
-  tn = bid % tiles_n;
+// Workgroup id -> (tile_m, tile_n). The dispatcher deals workgroup ids round robin to the 8 XCDs (XCD = id % 8,
+// in id order within an XCD), and each XCD has its own L2. The map gives XCD x the x-th contiguous share of a
+// grouped order in which 8 tile rows are walked column by column, so the 32 tiles an XCD runs at once form an 8 x 4
+// block: 12 operand panels for 32 tiles instead of ~36 for the row-major order. Measured on the 32768 x 15360 x 5120
+// GEMM: L2->fabric fetch 3.7 GiB instead of 11.3 GiB per launch, same duration.
+constexpr int kGroupRows = 8;
+
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n, per = total / 8, rem = total % 8, xcd = bid % 8, local = bid / 8;
+  const int logical = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+  const int group = kGroupRows * tiles_n, first = (logical / group) * kGroupRows;
+  const int rows = min(tiles_m - first, kGroupRows), within = logical % group;
+  tm = first + within % rows;
+  tn = within / rows;
 }
 
 // LDS rows are 64 bytes (four 16-byte chunks of K); chunk c of row r lives at c ^ ((r >> 1) & 3), which spreads the
@@ -155,7 +163,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   const int wm = wave & 1, wn = wave >> 1;  // 2 (m) x 4 (n) waves of 128 x 64
   const int sub = lane & 31, half = lane >> 5;
   int tm, tn;
-  tile_of(blockIdx.x, a.tiles_n, tm, tn);
+  tile_of(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
   const int m0 = tm * GBM, n0 = tn * GBN;
   const int rows_m = min(GBM, a.M - m0), rows_n = min(GBN, a.N - n0);
 
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   // Stage kt lives in slot kt % 4. Per stage: read the second K half while multiplying the first; wait for this
   // wave's loads of stage kt+1 (two more stages stay in flight) and for the reads of slot kt % 4; barrier; read
   // stage kt+1's first half, refill slot kt % 4 and multiply the second half, with the LDS reads and loads spread
-  // between the MFMAs. Skipping a refill (the tail) only makes the partial wait stricter, never looser.
+  // between the MFMAs. The wait relies on every iteration issuing the same 4 loads per wave.
   auto stage_body = [&](int kt, int refill) {
     const unsigned char HF_LDS* st = smem + (kt % kStages) * kStageBytes;
     read_frags(f1, st, wm, wn, 1, sub, half);
@@ -271,7 +279,9 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   int kt = 0;
   for (; kt < steady; ++kt) stage_body(kt, 0);
   for (; kt < nk; ++kt) {
-    int refill = 3;  // nothing: the stages a short K needs were issued up front
+    // Stages past the end load zeros, so every iteration issues exactly 4 loads per wave and vmcnt(8) always
+    // means "stage kt + 1 has landed" (with fewer loads behind it the wait would let it through early).
+    int refill = 0;
     if (lr_lds && kt == steady) refill = 1;
     if (lr_lds && kt == steady + 1) refill = 2;
     stage_body(kt, refill);
