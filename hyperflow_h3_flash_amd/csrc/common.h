@@ -57,6 +57,17 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// LDS row swizzles (16-byte chunk c of row r is stored at chunk c ^ f(r)). gfx950's LDS serves a ds_read_b128 16
+// lanes per cycle from 64 banks (256 bytes), so the rows read in one cycle must land on distinct 16-byte slots of a
+// 256-byte window; both swizzles also keep any 8 consecutive rows distinct within a 128-byte window. Measured: the
+// simpler c ^ ((r >> 1) & 3) for 64-byte rows stalled every fragment read on a 2-way bank conflict.
+__device__ __forceinline__ int swizzle64(int r, int c) {  // 64-byte rows: 4 chunks
+  return c ^ ((((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2));
+}
+__device__ __forceinline__ int swizzle128(int r, int c) {  // 128-byte rows: 8 chunks
+  return c ^ ((r ^ (r >> 3)) & 7);
+}
+
 // Buffer resource for raw (stride 0) buffer loads: offsets at or beyond `bytes` read as zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);

@@ -29,9 +29,11 @@ int log4_of(int32_t group) {
 void allow_large_lds() {
   static std::once_flag once;
   std::call_once(once, [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<false>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutI32>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<true>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16Lr>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<1>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
@@ -58,6 +60,20 @@ int check_gemm_operands(const int8_t* q, int64_t ldq, const int8_t* w, int64_t l
   return HF_OK;
 }
 
+// Workgroups for the persistent GEMM: one per CU of the current device (queried once per device), at most one per
+// tile.
+int gemm_grid(int64_t tiles) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  int n = dev < 64 ? cus[dev] : 0;
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    if (dev < 64) cus[dev] = n;
+  }
+  return (int)std::min<int64_t>(tiles, n);
+}
+
 int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream) {
   allow_large_lds();
   a.tiles_m = (a.M + hf::GBM - 1) / hf::GBM;
@@ -65,10 +81,13 @@ int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream) {
   const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
   if (tiles == 0) return HF_OK;
   if (tiles >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  const dim3 grid((unsigned)gemm_grid(tiles)), block(hf::kThreads);
   if (i32) {
-    hipLaunchKernelGGL(hf::int8_gemm_kernel<true>, dim3((unsigned)tiles), dim3(hf::kThreads), hf::kGemmLds, stream, a);
+    hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutI32>, grid, block, hf::kGemmLds, stream, a);
+  } else if (a.r > 0 && a.r <= 64) {
+    hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16Lr>, grid, block, hf::kGemmLds, stream, a);
   } else {
-    hipLaunchKernelGGL(hf::int8_gemm_kernel<false>, dim3((unsigned)tiles), dim3(hf::kThreads), hf::kGemmLds, stream, a);
+    hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16>, grid, block, hf::kGemmLds, stream, a);
   }
   return launch_status();
 }
@@ -177,6 +196,7 @@ int hf_int8_gemm_i32(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
   hf::GemmArgs a{};
   a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.out = acc; a.ldo = ldacc;
   a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  a.out_vec16 = (ldacc % 4) == 0;
   return launch_gemm(a, true, static_cast<hipStream_t>(stream));
 }
 

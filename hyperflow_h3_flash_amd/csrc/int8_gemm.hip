@@ -21,6 +21,8 @@
 // beyond the end read as zero through the buffer descriptor's range check. A rank <= 64 low-rank branch rides the
 // last two refills into the ring, so the epilogue reads its operands from LDS. The epilogue goes through LDS so the
 // output is written as whole 64-byte row segments, 16 bytes per lane.
+#include <type_traits>
+
 #include "common.h"
 
 namespace hf {
@@ -74,9 +76,8 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
   tn = within / rows;
 }
 
-// LDS rows are 64 bytes (four 16-byte chunks of K); chunk c of row r lives at c ^ ((r >> 1) & 3), which spreads the
-// 32 rows of one fragment read over all banks (measured conflict-free on gfx950 for ds_read_b128).
-__device__ __forceinline__ int swizzle(int r, int c) { return c ^ ((r >> 1) & 3); }
+// LDS rows are 64 bytes (four 16-byte chunks of K), swizzled with swizzle64.
+__device__ __forceinline__ int swizzle(int r, int c) { return swizzle64(r, c); }
 
 // Per-lane byte offsets of one wave's stage loads, computed once per tile. Load i of a wave fills LDS block
 // blk = first_blk + i (16 rows x 64 bytes): lane l fills row 16*blk + l/4, physical chunk l%4, from the logical chunk
@@ -95,25 +96,24 @@ struct StageOffsets {
   }
 };
 
-// Issue one wave's loads of a stage at K offset k0 into `dst` (LDS, wave-uniform). Chunks at or past K (only in a
-// partial last stage) read as zero; so does every load of a stage past the end (k0 >= K).
+// Issue one wave's loads of a stage at K offset k0 into `dst` (LDS, wave-uniform). A lane's 16-byte chunk sits at
+// the same K byte of the stage for every load (the swizzle of its row, 16*blk + lane/4, only sees row bits 1-3, i.e.
+// lane bits 3-5). Chunks at or past K read as zero (the offset moves past the descriptor), branch-free; so does every
+// load of a stage past the end (k0 >= K).
 template <int COUNT>
 __device__ __forceinline__ void load_stage(__amdgpu_buffer_rsrc_t rsrc, const StageOffsets<COUNT>& so, uint32_t oob,
                                            int k0, int K, unsigned char HF_LDS* dst, int first_blk, int lane) {
-  const bool partial = k0 + GBK > K;
+  const int kb = k0 + (swizzle(lane >> 2, lane & 3) << 4);
+  const uint32_t kadd = kb < K ? (uint32_t)k0 : oob;
 #pragma unroll
   for (int i = 0; i < COUNT; ++i) {
-    uint32_t voff = so.off[i] + (uint32_t)k0;
-    if (partial) {
-      const int kb = k0 + swizzle((first_blk + i) * 16 + (lane >> 2), lane & 3) * 16;
-      if (kb >= K) voff = oob;
-    }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + (first_blk + i) * 1024), 16, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + (first_blk + i) * 1024), 16, so.off[i] + kadd,
+                                             0, 0, 0);
   }
 }
 
 // The low-rank operands of a tile (u rows m or up rows n, rank r <= 64, as 128-byte rows of 8 chunks of 8 bf16,
-// chunk c of row i stored at c ^ (i & 7)) are loaded into a free ring slot: 256 rows x 128 bytes = 32 loads of
+// swizzled with swizzle128) are loaded into a free ring slot: 256 rows x 128 bytes = 32 loads of
 // 1 KiB, 4 per wave. Rows past the tile's valid rows and chunks past r read as zero.
 __device__ __forceinline__ void load_lowrank_rows(__amdgpu_buffer_rsrc_t rsrc, uint32_t oob, int64_t ld_bytes,
                                                   int rows_valid, int r, unsigned char HF_LDS* dst, int wave,
@@ -122,7 +122,7 @@ __device__ __forceinline__ void load_lowrank_rows(__amdgpu_buffer_rsrc_t rsrc, u
   for (int i = 0; i < 4; ++i) {
     const int blk = wave * 4 + i;
     const int row = blk * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ (row & 7);
+    const int c = swizzle128(row, lane & 7);
     const uint32_t voff = (row < rows_valid && c * 8 < r) ? (uint32_t)(row * ld_bytes + c * 16) : oob;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + blk * 1024), 16, voff, 0, 0, 0);
   }
@@ -135,7 +135,7 @@ struct Frags {
 
 __device__ __forceinline__ void read_frags(Frags& f, const unsigned char HF_LDS* stage, int wm, int wn, int ks,
                                            int sub, int half) {
-  const int chunk = swizzle(sub, 2 * ks + half) * 16;  // (row >> 1) & 3 == (sub >> 1) & 3: blocks start at 32k
+  const int chunk = swizzle(sub, 2 * ks + half) * 16;  // blocks start at multiples of 32 rows: f(row) == f(sub)
   const unsigned char HF_LDS* As = stage;
   const unsigned char HF_LDS* Bs = stage + kAStage;
 #pragma unroll
@@ -154,7 +154,64 @@ __device__ __forceinline__ void mma(v16i (&acc)[2][4], const Frags& f) {
 
 #define HF_BARRIER() asm volatile("s_barrier" ::: "memory")
 
-template <bool I32OUT>
+// s_waitcnt vmcnt(n) for the wave-uniform counts the persistent loop uses (an unlisted count waits for everything,
+// which is always safe). The loop's accounting relies on vector memory operations completing in issue order (loads,
+// LDS-DMA loads and stores share one in-order counter on gfx9).
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n) {
+    case 8: asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)" ::: "memory"); break;
+    case 26: asm volatile("s_waitcnt vmcnt(26) lgkmcnt(0)" ::: "memory"); break;
+    case 28: asm volatile("s_waitcnt vmcnt(28) lgkmcnt(0)" ::: "memory"); break;
+    case 40: asm volatile("s_waitcnt vmcnt(40) lgkmcnt(0)" ::: "memory"); break;
+    case 44: asm volatile("s_waitcnt vmcnt(44) lgkmcnt(0)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); break;
+  }
+}
+
+// One output tile's operand source: the q rows m0.. and w rows n0.. as buffer descriptors (rows past the matrix and
+// every row of a tile past the last one read as zero) and the per-lane stage offsets.
+struct TileSrc {
+  int m0, n0, rows_m, rows_n;
+  uint32_t bytes_q, bytes_w;
+  __amdgpu_buffer_rsrc_t rq, rw;
+  StageOffsets<2> offq, offw;
+};
+
+__device__ __forceinline__ void tile_src(const GemmArgs& a, int id, int wave, int lane, TileSrc& t) {
+  int tm = 0, tn = 0;
+  const bool live = id < a.tiles_m * a.tiles_n;
+  if (live) tile_of(id, a.tiles_m, a.tiles_n, tm, tn);
+  t.m0 = tm * GBM;
+  t.n0 = tn * GBN;
+  t.rows_m = live ? min(GBM, a.M - t.m0) : 0;
+  t.rows_n = live ? min(GBN, a.N - t.n0) : 0;
+  t.bytes_q = (uint32_t)(t.rows_m * a.ldq);
+  t.bytes_w = (uint32_t)(t.rows_n * a.ldw);
+  t.rq = make_rsrc(a.q + (int64_t)t.m0 * a.ldq, t.bytes_q);
+  t.rw = make_rsrc(a.w + (int64_t)t.n0 * a.ldw, t.bytes_w);
+  t.offq.init(t.bytes_q, a.ldq, t.rows_m, wave * 2, lane);
+  t.offw.init(t.bytes_w, a.ldw, t.rows_n, wave * 2, lane);
+}
+
+// Stage kt of tile t into ring slot `slot`: 4 loads per wave (2 of q, 2 of w).
+__device__ __forceinline__ void load_tile_stage(const TileSrc& t, const GemmArgs& a, int kt,
+                                                unsigned char HF_LDS* slot, int wave, int lane) {
+  load_stage<2>(t.rq, t.offq, t.bytes_q, kt * GBK, a.K, slot, wave * 2, lane);
+  load_stage<2>(t.rw, t.offw, t.bytes_w, kt * GBK, a.K, slot + kAStage, wave * 2, lane);
+}
+
+// Output modes: int32 accumulators; bf16 with the dequantization (and, for r > 64, the low-rank term from global
+// memory) and bias; bf16 with a rank <= 64 low-rank term whose operands ride the ring.
+constexpr int kOutI32 = 0, kOutBf16 = 1, kOutBf16Lr = 2;
+
+// Persistent kernel: one workgroup per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... The ring of 4 stages
+// runs continuously across tiles: the last 4 iterations of a tile refill their slots with the next tile's first
+// stages (after the tile's u and up tiles in low-rank mode), so a tile starts with its operands in flight and the
+// epilogue's output stores drain while the next tile computes. Every ring step issues exactly 4 loads per wave
+// (past the last tile they read zeros), which keeps every wait a fixed vmcnt.
+template <int OUT>
 __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[];
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)smem_raw;
@@ -162,266 +219,288 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps LDS addresses scalar
   const int wm = wave & 1, wn = wave >> 1;  // 2 (m) x 4 (n) waves of 128 x 64
   const int sub = lane & 31, half = lane >> 5;
-  int tm, tn;
-  tile_of(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
-  const int m0 = tm * GBM, n0 = tn * GBN;
-  const int rows_m = min(GBM, a.M - m0), rows_n = min(GBN, a.N - n0);
-
-  const uint32_t bytes_q = (uint32_t)(rows_m * a.ldq), bytes_w = (uint32_t)(rows_n * a.ldw);
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q + (int64_t)m0 * a.ldq, bytes_q);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + (int64_t)n0 * a.ldw, bytes_w);
-
-  StageOffsets<2> offq, offw;
-  offq.init(bytes_q, a.ldq, rows_m, wave * 2, lane);
-  offw.init(bytes_w, a.ldw, rows_n, wave * 2, lane);
-  // Stage kt into slot kt % 4; a stage past the end (kt >= nk) loads zeros, which keeps the loop branch-free.
-  auto issue_stage = [&](int kt) {
-    unsigned char HF_LDS* st = smem + (kt % kStages) * kStageBytes;
-    load_stage<2>(rq, offq, bytes_q, kt * GBK, a.K, st, wave * 2, lane);
-    load_stage<2>(rw, offw, bytes_w, kt * GBK, a.K, st + kAStage, wave * 2, lane);
-  };
-
-  // The epilogue's per-row and per-column factors, loaded into registers now and parked in LDS beside the ring when
-  // the epilogue starts, so no epilogue instruction waits on global memory. Threads 0..255 take row m0 + t and
-  // column n0 + t (sx, wscale); threads 256..511 take the bias of column n0 + t - 256.
+  constexpr bool kLr = OUT == kOutBf16Lr;
+  constexpr int kParamLoads = OUT == kOutI32 ? 0 : 2;  // per thread and tile
+  constexpr int kFastStores = OUT == kOutI32 ? 32 : 16;  // per wave and tile, full tiles only
   float HF_LDS* params = (float HF_LDS*)(smem + kRingBytes);
-  float p_val = 0.0f;
-  uint32_t p_bias = 0;
   const int pt = threadIdx.x & 255;
-  if (!I32OUT) {
-    // Branch-free (clamped indices, a stand-in array when there is no bias) so no wait lands here; rows and columns
-    // past the edge are masked when the values are parked.
-    if (threadIdx.x < 256) {
-      p_val = a.sx[min(m0 + pt, a.M - 1)];
-      p_bias = __float_as_uint(a.sw[min(n0 + pt, a.N - 1)]);
-    } else {
-      const uint16_t* bsrc = a.bias ? a.bias : reinterpret_cast<const uint16_t*>(a.sw);
-      p_bias = bsrc[min(n0 + pt, a.N - 1)];
-    }
-  }
+  auto slot_at = [&](int step) { return smem + (step & (kStages - 1)) * kStageBytes; };
 
-  v16i acc[2][4];
+  // K steps per tile, at least 7 so the three first steps, the steady loop and the four refill steps never overlap
+  // (stages past K read zeros and add nothing).
+  const int nk = max((a.K + GBK - 1) / GBK, kStages + 3);
+  const int total = a.tiles_m * a.tiles_n;
+  int id = blockIdx.x;
+  TileSrc cur;
+  tile_src(a, id, wave, lane, cur);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (v16i){0};
+  for (int j = 0; j < kStages; ++j) load_tile_stage(cur, a, j, slot_at(j), wave, lane);
 
-  const int nk = (a.K + GBK - 1) / GBK;
-  // Prologue: stages 0..3 in flight (4 loads per wave per stage), wait for stage 0.
-  issue_stage(0);
-  issue_stage(1);
-  issue_stage(2);
-  issue_stage(3);
-  asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-  HF_BARRIER();
+  int g = 0;             // ring step of the current tile's stage 0
+  bool stores_behind = false;  // the previous tile's epilogue left kFastStores stores behind its stage 3
   Frags f0, f1;
-  read_frags(f0, smem, wm, wn, 0, sub, half);
+  v16i acc[2][4];
 
-  // With a rank <= 64 low-rank branch, the u tile [256 m][r] and the up tile [256 n][r] take the places of the
-  // stage loads the last iterations would not need; they land in the ring slots nk % 4 and (nk + 1) % 4.
-  const bool lr_lds = !I32OUT && a.r > 0 && a.r <= 64 && nk >= kStages;
-  __amdgpu_buffer_rsrc_t ru = rq, rup = rw;
-  uint32_t bytes_u = 0, bytes_up = 0;
-  if (lr_lds) {
-    bytes_u = (uint32_t)(rows_m * a.ldu * 2);
-    bytes_up = (uint32_t)(rows_n * a.ldup * 2);
-    ru = make_rsrc(a.u + (int64_t)m0 * a.ldu, bytes_u);
-    rup = make_rsrc(a.up + (int64_t)n0 * a.ldup, bytes_up);
-  }
+  // One tile; SPILL counts the stores the previous epilogue issued after this tile's stage 3 (they precede the
+  // parameter loads), so every wait count below is a constant.
+  auto tile = [&](auto spill_tag) -> bool {
+    constexpr int spill = decltype(spill_tag)::value;
+    const int next_id = id + gridDim.x;
+    TileSrc nxt;
+    tile_src(a, next_id, wave, lane, nxt);
 
-  // Stage kt lives in slot kt % 4. Per stage: read the second K half while multiplying the first; wait for this
-  // wave's loads of stage kt+1 (two more stages stay in flight) and for the reads of slot kt % 4; barrier; read
-  // stage kt+1's first half, refill slot kt % 4 and multiply the second half, with the LDS reads and loads spread
-  // between the MFMAs. The wait relies on every iteration issuing the same 4 loads per wave.
-  auto stage_body = [&](int kt, int refill) {
-    const unsigned char HF_LDS* st = smem + (kt % kStages) * kStageBytes;
-    read_frags(f1, st, wm, wn, 1, sub, half);
-    mma(acc, f0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
-    __builtin_amdgcn_sched_barrier(0);  // every MFMA of the first half issues before the wait and barrier
-    asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+    // Stage 0 landed (stages 1..3 and the previous tile's stores may still be in flight).
+    wait_vm(12 + spill);
     HF_BARRIER();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(f0, smem + ((kt + 1) % kStages) * kStageBytes, wm, wn, 0, sub, half);
-    unsigned char HF_LDS* slot = smem + (kt % kStages) * kStageBytes;
-    if (refill == 0) {
-      load_stage<2>(rq, offq, bytes_q, (kt + 4) * GBK, a.K, slot, wave * 2, lane);
-      load_stage<2>(rw, offw, bytes_w, (kt + 4) * GBK, a.K, slot + kAStage, wave * 2, lane);
-    } else if (refill == 1) {
-      load_lowrank_rows(ru, bytes_u, a.ldu * 2, rows_m, a.r, slot, wave, lane);
-    } else if (refill == 2) {
-      load_lowrank_rows(rup, bytes_up, a.ldup * 2, rows_n, a.r, slot, wave, lane);
-    }
-    mma(acc, f1);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // VMEM (stage load)
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  const int steady = nk - kStages;  // iterations whose refill is a real stage
-  int kt = 0;
-  for (; kt < steady; ++kt) stage_body(kt, 0);
-  for (; kt < nk; ++kt) {
-    // Stages past the end load zeros, so every iteration issues exactly 4 loads per wave and vmcnt(8) always
-    // means "stage kt + 1 has landed" (with fewer loads behind it the wait would let it through early).
-    int refill = 0;
-    if (lr_lds && kt == steady) refill = 1;
-    if (lr_lds && kt == steady + 1) refill = 2;
-    stage_body(kt, refill);
-  }
-  // Zero-fill loads past the end may still be landing in the ring; the epilogue reuses it.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    read_frags(f0, slot_at(g), wm, wn, 0, sub, half);
 
-  // Output layout of a 32x32 block: lane holds column j = lane % 32 (the row m here) and, in register v, row
-  // i = 8*(v/4) + 4*(lane/32) + v%4 (the column n here): four consecutive n per group of four registers.
-  if constexpr (I32OUT) {
-    int32_t* out = static_cast<int32_t*>(a.out);
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      const int m = m0 + wm * 128 + jb * 32 + sub;
-      if (m >= a.M) continue;
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = n0 + wn * 64 + ib * 32 + 8 * g + 4 * half;
-          int32_t* dst = out + (int64_t)m * a.ldo + n;
-          const v16i& c = acc[ib][jb];
-          if (n + 3 < a.N && ((a.ldo & 3) == 0)) {
-            *reinterpret_cast<int4*>(dst) = make_int4(c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]);
-          } else {
-            for (int e = 0; e < 4; ++e)
-              if (n + e < a.N) dst[e] = c[4 * g + e];
-          }
-        }
+    // The epilogue's per-row and per-column factors, loaded now and parked in LDS when the epilogue starts:
+    // threads 0..255 take sx of row m0 + t and wscale of column n0 + t, threads 256..511 the bias of column
+    // n0 + t - 256 (and a second, unused load so every wave issues the same count). Clamped, branch-free.
+    float p_val = 0.0f;
+    uint32_t p_bias = 0;
+    if (OUT != kOutI32) {
+      const int mr = min(cur.m0 + pt, a.M - 1), nc = min(cur.n0 + pt, a.N - 1);
+      const uint16_t* bsrc = a.bias ? a.bias : reinterpret_cast<const uint16_t*>(a.sw);
+      p_val = a.sx[mr];
+      p_bias = threadIdx.x < 256 ? __float_as_uint(a.sw[nc]) : (uint32_t)bsrc[nc];
     }
-  } else {
-    // Dequantize one 32-wide block of output columns at a time (add the low-rank product on bf16 MFMA and the
-    // bias), round to bf16 and park it in LDS (this wave's 128 x 32 block: rows of 64 bytes, 16-byte chunk c of row
-    // i at c ^ ((i >> 1) & 3)), then write 64-byte row segments, 16 bytes per lane, 16 rows per instruction. The
-    // staging uses the two ring slots the low-rank tiles do not: waves 0-3 slot (nk + 2) % 4, waves 4-7 slot
-    // (nk + 3) % 4, 8 KiB each.
-    if (threadIdx.x < 256) {
-      params[pt] = (m0 + pt < a.M) ? p_val : 0.0f;
-      params[256 + pt] = (n0 + pt < a.N) ? __uint_as_float(p_bias) : 0.0f;
+    constexpr int early = 8 + spill + kParamLoads;  // wait count while those operations sit behind the stage
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = (v16i){0};
+
+    // Step kt: read the second K half of slot kt while multiplying the first; wait until stage kt + 1 landed (for
+    // this wave) and the slot's reads returned; barrier; read stage kt + 1's first half, refill slot kt and multiply
+    // the second half, with LDS reads and loads spread between the MFMAs.
+    auto step = [&](int kt, int vm, bool read_next, auto&& refill) {
+      read_frags(f1, slot_at(g + kt), wm, wn, 1, sub, half);
+      mma(acc, f0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
+      __builtin_amdgcn_sched_barrier(0);  // every MFMA of the first half issues before the wait and barrier
+      wait_vm(vm);
+      HF_BARRIER();
+      __builtin_amdgcn_sched_barrier(0);
+      if (read_next) read_frags(f0, slot_at(g + kt + 1), wm, wn, 0, sub, half);
+      refill(slot_at(g + kt));
+      mma(acc, f1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // VMEM (stage load)
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto own_stage = [&](int kt) {
+      return [&, kt](unsigned char HF_LDS* s) { load_tile_stage(cur, a, kt, s, wave, lane); };
+    };
+    auto next_stage = [&](int kt) {
+      return [&, kt](unsigned char HF_LDS* s) { load_tile_stage(nxt, a, kt, s, wave, lane); };
+    };
+
+    // Steps 0..nk-5 refill with this tile's stages 4..nk-1; the first three still have the stores and parameter
+    // loads behind the stage they wait for.
+    step(0, early, true, own_stage(kStages));
+    step(1, early, true, own_stage(kStages + 1));
+    step(2, early, true, own_stage(kStages + 2));
+    int kt = 3;
+    for (; kt < nk - kStages; ++kt) step(kt, 8, true, own_stage(kt + kStages));
+    // The last four steps refill with the tile's low-rank operands and the next tile's first stages.
+    const __amdgpu_buffer_rsrc_t ru =
+        make_rsrc(a.u + (int64_t)cur.m0 * a.ldu, kLr ? (uint32_t)(cur.rows_m * a.ldu * 2) : 0u);
+    const __amdgpu_buffer_rsrc_t rup =
+        make_rsrc(a.up + (int64_t)cur.n0 * a.ldup, kLr ? (uint32_t)(cur.rows_n * a.ldup * 2) : 0u);
+    if constexpr (kLr) {
+      step(kt, 8, true, [&](unsigned char HF_LDS* s) {
+        load_lowrank_rows(ru, (uint32_t)(cur.rows_m * a.ldu * 2), a.ldu * 2, cur.rows_m, a.r, s, wave, lane);
+      });
+      step(kt + 1, 8, true, [&](unsigned char HF_LDS* s) {
+        load_lowrank_rows(rup, (uint32_t)(cur.rows_n * a.ldup * 2), a.ldup * 2, cur.rows_n, a.r, s, wave, lane);
+      });
+      step(kt + 2, 8, true, next_stage(0));
+      step(kt + 3, 8, false, next_stage(1));
     } else {
-      params[512 + pt] = (n0 + pt < a.N && a.bias) ? __uint_as_float(p_bias << 16) : 0.0f;
+      step(kt, 8, true, next_stage(0));
+      step(kt + 1, 8, true, next_stage(1));
+      step(kt + 2, 8, true, next_stage(2));
+      step(kt + 3, 8, false, next_stage(3));
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    HF_BARRIER();
-    float sxv[4];
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb) sxv[jb] = params[wm * 128 + jb * 32 + sub];
-    const unsigned char HF_LDS* u_lds = smem + (nk % kStages) * kStageBytes;
-    const unsigned char HF_LDS* up_lds = smem + ((nk + 1) % kStages) * kStageBytes;
-    unsigned char HF_LDS* tile =
-        smem + ((nk + 2 + (wave >> 2)) % kStages) * kStageBytes + (wave & 3) * (128 * 64);
-    const bool has_bias = a.bias != nullptr;
-    uint16_t* out = static_cast<uint16_t*>(a.out);
-#pragma unroll
-    for (int ib = 0; ib < 2; ++ib) {
-      const int nb = n0 + wn * 64 + ib * 32;
-      float ws[16], bv[16];
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int nl = wn * 64 + ib * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-        ws[v] = params[256 + nl];
-        bv[v] = params[512 + nl];
-      }
-      v16f c[4];
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float t = (float)acc[ib][jb][v] * sxv[jb];
-          c[jb][v] = t * ws[v];
-        }
-      if (lr_lds) {
-        // Low-rank term from the LDS tiles: first operand up[n, :], second u[m, :], 16 ranks per MFMA.
-        const int nl = wn * 64 + ib * 32 + sub;
-        for (int kk = 0; kk < a.r; kk += 16) {
-          const int chunk = kk / 8 + half;
-          const v8bf pf = *(const v8bf HF_LDS*)(up_lds + nl * 128 + ((chunk ^ (nl & 7)) * 16));
-#pragma unroll
-          for (int jb = 0; jb < 4; ++jb) {
-            const int ml = wm * 128 + jb * 32 + sub;
-            const v8bf uf = *(const v8bf HF_LDS*)(u_lds + ml * 128 + ((chunk ^ (ml & 7)) * 16));
-            c[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[jb], 0, 0, 0);
-          }
-        }
-      } else if (a.r > 0) {
-        // Ranks above 64 (or a K too short to carry them in the ring): the same product from global memory.
-        const int nrow = min(nb + sub, a.N - 1);
-        for (int kk = 0; kk < a.r; kk += 16) {
-          const int k = kk + 8 * half;
-          const v8bf pf = (k < a.r) ? *reinterpret_cast<const v8bf*>(a.up + (int64_t)nrow * a.ldup + k) : (v8bf){0};
-#pragma unroll
-          for (int jb = 0; jb < 4; ++jb) {
-            const int mrow = min(m0 + wm * 128 + jb * 32 + sub, a.M - 1);
-            const v8bf uf = (k < a.r) ? *reinterpret_cast<const v8bf*>(a.u + (int64_t)mrow * a.ldu + k) : (v8bf){0};
-            c[jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[jb], 0, 0, 0);
-          }
-        }
-      }
+
+    // ------------------------------------------------------------------------------------------------ epilogue
+    // Output layout of a 32x32 block: lane holds column j = lane % 32 (the row m here) and, in register v, row
+    // i = 8*(v/4) + 4*(lane/32) + v%4 (the column n here): four consecutive n per group of four registers.
+    const int m0 = cur.m0, n0 = cur.n0;
+    bool full;
+    if constexpr (OUT == kOutI32) {
+      full = cur.rows_m == GBM && cur.rows_n == GBN && a.out_vec16;
+      int32_t* out = static_cast<int32_t*>(a.out);
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
-        const int rr = jb * 32 + sub;
+        const int m = m0 + wm * 128 + jb * 32 + sub;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float v[4];
+        for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            v[e] = c[jb][4 * g + e];
-            if (has_bias) v[e] = v[e] + bv[4 * g + e];
+          for (int gq = 0; gq < 4; ++gq) {
+            const int n = n0 + wn * 64 + ib * 32 + 8 * gq + 4 * half;
+            int32_t* dst = out + (int64_t)m * a.ldo + n;
+            const v16i& c = acc[ib][jb];
+            if (full) {
+              *reinterpret_cast<v4i*>(dst) = (v4i){c[4 * gq], c[4 * gq + 1], c[4 * gq + 2], c[4 * gq + 3]};
+            } else if (m < a.M) {
+              for (int e = 0; e < 4; ++e)
+                if (n + e < a.N) dst[e] = c[4 * gq + e];
+            }
           }
-          const int chunk = g ^ ((rr >> 1) & 3);
-          typedef unsigned int v2u __attribute__((ext_vector_type(2)));
-          *(v2u HF_LDS*)(tile + rr * 64 + chunk * 16 + 8 * half) = (v2u){pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      }
+    } else {
+      full = cur.rows_m == GBM && cur.rows_n == GBN && a.out_vec16 && (kLr || a.r == 0);
+      if (threadIdx.x < 256) {
+        params[pt] = (m0 + pt < a.M) ? p_val : 0.0f;
+        params[256 + pt] = (n0 + pt < a.N) ? __uint_as_float(p_bias) : 0.0f;
+      } else {
+        params[512 + pt] = (n0 + pt < a.N && a.bias) ? __uint_as_float(p_bias << 16) : 0.0f;
+      }
+      // Low-rank mode: the up tile (step g + nk + 1) has landed once only the next tile's stages 0 and 1 are
+      // behind it. The barrier also publishes the parameters.
+      if constexpr (kLr) {
+        wait_vm(8);
+      } else {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      }
+      HF_BARRIER();
+      float sxv[4];
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) sxv[jb] = params[wm * 128 + jb * 32 + sub];
+      const unsigned char HF_LDS* u_lds = slot_at(g + nk);
+      const unsigned char HF_LDS* up_lds = slot_at(g + nk + 1);
+      v16f c[2][4];
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int nl = wn * 64 + ib * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            c[ib][jb][v] = ((float)acc[ib][jb][v] * sxv[jb]) * params[256 + nl];
+          }
+        if constexpr (kLr) {
+          // Low-rank term from the LDS tiles (rows of 128 bytes, swizzle128): first operand
+          // up[n, :], second u[m, :], 16 ranks per MFMA, accumulated onto the dequantized values.
+          const int nl = wn * 64 + ib * 32 + sub;
+          for (int kk = 0; kk < a.r; kk += 16) {
+            const int chunk = kk / 8 + half;
+            const v8bf pf = *(const v8bf HF_LDS*)(up_lds + nl * 128 + swizzle128(nl, chunk) * 16);
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+              const int ml = wm * 128 + jb * 32 + sub;
+              const v8bf uf = *(const v8bf HF_LDS*)(u_lds + ml * 128 + swizzle128(ml, chunk) * 16);
+              c[ib][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[ib][jb], 0, 0, 0);
+            }
+          }
+        } else if (a.r > 0) {
+          // Ranks above 64: the same product from global memory.
+          const int nrow = min(n0 + wn * 64 + ib * 32 + sub, a.N - 1);
+          for (int kk = 0; kk < a.r; kk += 16) {
+            const int k = kk + 8 * half;
+            const v8bf pf =
+                (k < a.r) ? *reinterpret_cast<const v8bf*>(a.up + (int64_t)nrow * a.ldup + k) : (v8bf){0};
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+              const int mrow = min(m0 + wm * 128 + jb * 32 + sub, a.M - 1);
+              const v8bf uf =
+                  (k < a.r) ? *reinterpret_cast<const v8bf*>(a.u + (int64_t)mrow * a.ldu + k) : (v8bf){0};
+              c[ib][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[ib][jb], 0, 0, 0);
+            }
+          }
         }
       }
-      wave_lds_sync();
+      if constexpr (kLr) {
+        // Every wave is done with the u and up slots: refill them with the next tile's stages 2 and 3.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        HF_BARRIER();
+        load_tile_stage(nxt, a, 2, slot_at(g + nk), wave, lane);
+        load_tile_stage(nxt, a, 3, slot_at(g + nk + 1), wave, lane);
+      }
+      // Bias, bf16, and the stores: after one exchange between the lane halves (v_permlane32_swap: lanes 32..63 of
+      // the first operand <-> lanes 0..31 of the second), lane (sub, h) holds columns 16h..16h+15 of row sub of
+      // the block, 32 contiguous bytes written as two 16-byte stores; the two halves cover the row's 64 bytes.
+      uint16_t* out = static_cast<uint16_t*>(a.out);
+      const bool has_bias = a.bias != nullptr;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int rr = i * 16 + (lane >> 2);
-        const int p = lane & 3;
-        const int cc = p ^ ((rr >> 1) & 3);
-        const v4i v = *(const v4i HF_LDS*)(tile + rr * 64 + p * 16);
-        const int m = m0 + wm * 128 + rr;
-        const int n = nb + cc * 8;
-        if (m < a.M) {
+      for (int ib = 0; ib < 2; ++ib) {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          uint32_t pk[4][2];
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = c[ib][jb][4 * gq + e];
+              if (has_bias) v[e] = v[e] + params[512 + wn * 64 + ib * 32 + 8 * gq + 4 * half + e];
+            }
+            pk[gq][0] = pack_bf16x2(v[0], v[1]);
+            pk[gq][1] = pack_bf16x2(v[2], v[3]);
+          }
+#pragma unroll
+          for (int w = 0; w < 2; ++w) {
+            const auto s02 = __builtin_amdgcn_permlane32_swap(pk[0][w], pk[2][w], false, false);
+            const auto s13 = __builtin_amdgcn_permlane32_swap(pk[1][w], pk[3][w], false, false);
+            pk[0][w] = s02[0];
+            pk[2][w] = s02[1];
+            pk[1][w] = s13[0];
+            pk[3][w] = s13[1];
+          }
+          const int m = m0 + wm * 128 + jb * 32 + sub;
+          const int n = n0 + wn * 64 + ib * 32 + 16 * half;
           uint16_t* dst = out + (int64_t)m * a.ldo + n;
-          if (a.out_vec16 && n + 7 < a.N) {
-            *reinterpret_cast<v4i*>(dst) = v;
-          } else {
-            const uint32_t wds[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
-            for (int e = 0; e < 8; ++e)
+          const v4i lo = (v4i){(int)pk[0][0], (int)pk[0][1], (int)pk[2][0], (int)pk[2][1]};
+          const v4i hi = (v4i){(int)pk[1][0], (int)pk[1][1], (int)pk[3][0], (int)pk[3][1]};
+          if (full) {
+            *reinterpret_cast<v4i*>(dst) = lo;
+            *reinterpret_cast<v4i*>(dst + 8) = hi;
+          } else if (m < a.M) {
+            const uint32_t wds[8] = {pk[0][0], pk[0][1], pk[2][0], pk[2][1], pk[1][0], pk[1][1], pk[3][0], pk[3][1]};
+            for (int e = 0; e < 16; ++e)
               if (n + e < a.N) dst[e] = (uint16_t)(wds[e >> 1] >> (16 * (e & 1)));
           }
         }
       }
-      wave_lds_sync();  // the block is overwritten by the next one
     }
+    // A partial tile's guarded stores (and the r > 64 global reads) are not a fixed count: drain everything.
+    if (!full) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    g += nk + (kLr ? 2 : 0);
+    id = next_id;
+    cur = nxt;
+    return full;
+  };
+  while (id < total) {
+    stores_behind = stores_behind ? tile(std::integral_constant<int, kFastStores>{})
+                                  : tile(std::integral_constant<int, 0>{});
   }
+  // Zero-fill loads for the tile after the last may still be landing in LDS.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template __global__ void int8_gemm_kernel<false>(GemmArgs);
-template __global__ void int8_gemm_kernel<true>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutI32>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16Lr>(GemmArgs);
 
 }  // namespace hf

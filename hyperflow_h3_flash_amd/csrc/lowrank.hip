@@ -23,9 +23,8 @@ constexpr int kLrStages = 6;
 constexpr int kLrLds = kLrStages * kLrStageBytes;     // 144 KiB
 constexpr int kLrThreads = 256;
 
-// LDS rows are 128 bytes (eight 16-byte chunks); chunk c of row i lives at c ^ (i & 7), so the 32 rows of one
-// fragment read (16 bytes each) cover all banks.
-__device__ __forceinline__ int lr_swizzle(int row, int c) { return c ^ (row & 7); }
+// LDS rows are 128 bytes (eight 16-byte chunks), swizzled with swizzle128 so fragment reads are conflict-free.
+__device__ __forceinline__ int lr_swizzle(int row, int c) { return swizzle128(row, c); }
 
 // One wave's share of a stage: `count` loads of 1 KiB (8 rows x 128 bytes) starting at LDS block `first_blk`.
 // Rows at or past `rows_valid`, and chunks at or past K, read as zero (offset `oob` is past the descriptor).
