@@ -41,7 +41,20 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=32768, help="row sample for the CPU baseline")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="only copy a 1 GiB device buffer 3 times (calibrates the HBM byte counters) and exit")
     return p.parse_args()
+
+
+def copy_probe(torch):
+    """Three device-to-device copies of 1 GiB: the known-size workload that scales FETCH_SIZE / WRITE_SIZE."""
+    dev = torch.device("cuda:0")
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_per_launch": src.numel() * 4}), flush=True)
 
 
 def make_inputs(torch, dev, seed=0):
@@ -106,6 +119,10 @@ def main():
               "the linear shards by rows with no communication, see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     import torch
+
+    if args.copy_probe:
+        copy_probe(torch)
+        return
 
     from hyperflow_h3_flash_amd import Int8RotLinear
     from hyperflow_h3_flash_amd.int8 import _kernels
