@@ -8,19 +8,24 @@
 //   y[m, n]   = bf16((f32(acc) * sx[m]) * sw[n] + sum_j u[m, j] * up[n, j] + bias[n])
 // With no low-rank branch and no bias the output is bitwise the reference's.
 //
-// Tiling: 256 (m) x 256 (n) output tile per workgroup (one per CU), K in stages of 64 bytes, 8 waves (two per SIMD,
-// so one wave's barrier wait and load issue run under the other's MFMAs) in a 2 (m) x 4 (n) grid, each wave a
-// 128 x 64 sub-tile of 4 x 2 v_mfma_i32_32x32x32_i8 blocks (128 accumulator registers). The
-// MFMA's first operand is the weight (its rows are the output columns n) and the second the activation, so each
-// lane ends with four consecutive n of one row m and reads one activation scale per block.
+// Tiling: 256 (m) x 256 (n) output tile per workgroup (one workgroup per CU, persistent), 8 waves (two per SIMD) in
+// a 2 (m) x 4 (n) grid, each a 128 x 64 sub-tile of 4 x 2 v_mfma_i32_32x32x32_i8 blocks (128 accumulator
+// registers). The MFMA's first operand is the weight (its rows are the output columns n) and the second the
+// activation, so each lane ends with four consecutive n of one row m.
 //
-// Operands go global -> LDS with buffer_load ... lds (16 bytes per lane, no VGPR round trip) into a 4-stage ring
-// (128 KiB); the waits are partial (vmcnt counts the loads still allowed in flight) and the barrier carries no
-// memory fence, so three stages stay in flight while one is consumed. MFMA operands are double-buffered in
-// registers: the LDS reads of one 32-byte K step overlap the MFMAs of the previous one. Out-of-range rows and K
-// beyond the end read as zero through the buffer descriptor's range check. A rank <= 64 low-rank branch rides the
-// last two refills into the ring, so the epilogue reads its operands from LDS. The epilogue goes through LDS so the
-// output is written as whole 64-byte row segments, 16 bytes per lane.
+// Operands: K is consumed in stages of 128 bytes. A stage (256 rows of q and 256 rows of w, 128 bytes each: 64 KiB)
+// goes global -> LDS with buffer_load ... lds, 16 bytes per lane, 8 lanes per row, so every load instruction moves
+// 8 whole 128-byte lines (half-line requests measured 11 % slower: the texture-address FIFOs fill). Two stage slots
+// alternate (double buffering): the loads of stage s + 2 are issued, two at a time between MFMAs, while stage s + 1
+// is multiplied. Waits are exact vmcnt counts; the barrier carries no memory fence. MFMA operands are
+// double-buffered in registers (the LDS reads of one 32-byte K step overlap the MFMAs of the previous one).
+// Out-of-range rows and K beyond the end read as zero through the buffer descriptor's range check.
+//
+// The slot of a tile's second-to-last stage is the epilogue's: it receives the tile's low-rank operands (u rows m
+// and up rows n, rank <= 64, one 128-byte row each) while the last stage is multiplied, then stages the bf16 output
+// so each store instruction writes 8 whole 128-byte lines. Meanwhile the other slot already receives the next
+// tile's first stage, and the next tile's second stage is issued into the epilogue slot once the stores are out:
+// loads never stop at a tile boundary.
 #include <type_traits>
 
 #include "common.h"
@@ -29,16 +34,16 @@ namespace hf {
 
 constexpr int GBM = 256;                          // activation rows (m) per workgroup tile
 constexpr int GBN = 256;                          // weight rows (n) per workgroup tile
-constexpr int GBK = 64;                           // K bytes per pipeline stage
-constexpr int kStages = 4;                        // LDS ring depth
-constexpr int kAStage = GBM * GBK;                // 16 KiB
-constexpr int kBStage = GBN * GBK;                // 16 KiB
-constexpr int kStageBytes = kAStage + kBStage;    // 32 KiB
-constexpr int kRingBytes = kStages * kStageBytes; // 128 KiB; the epilogue reuses it as a 256 x 256 bf16 tile
-constexpr int kParamBytes = 3 * 256 * 4;          // the tile's sx, wscale and bias (fp32), staged at kernel start
+constexpr int GBK = 128;                          // K bytes per pipeline stage
+constexpr int kAStage = GBM * GBK;                // 32 KiB
+constexpr int kBStage = GBN * GBK;                // 32 KiB
+constexpr int kSlotBytes = kAStage + kBStage;     // 64 KiB
+constexpr int kRingBytes = 2 * kSlotBytes;        // 128 KiB
+constexpr int kParamBytes = 3 * 256 * 4;          // the tile's sx, wscale and bias (fp32)
 constexpr int kGemmLds = kRingBytes + kParamBytes;
-constexpr int kWaves = 8;                         // 2 per SIMD: one wave's barrier and load issue hide under the other's MFMAs
+constexpr int kWaves = 8;                         // 2 per SIMD: one wave's barrier wait hides under the other's MFMAs
 constexpr int kThreads = 64 * kWaves;
+constexpr int kStageLoads = 8;                    // load instructions per wave per stage (4 of q, 4 of w)
 
 struct GemmArgs {
   const int8_t* q;
@@ -63,8 +68,7 @@ struct GemmArgs {
 // Workgroup id -> (tile_m, tile_n). The dispatcher deals workgroup ids round robin to the 8 XCDs (XCD = id % 8,
 // in id order within an XCD), and each XCD has its own L2. The map gives XCD x the x-th contiguous share of a
 // grouped order in which 8 tile rows are walked column by column, so the 32 tiles an XCD runs at once form an 8 x 4
-// block: 12 operand panels for 32 tiles instead of ~36 for the row-major order. Measured on the 32768 x 15360 x 5120
-// GEMM: L2->fabric fetch 3.7 GiB instead of 11.3 GiB per launch, same duration.
+// block: 12 operand panels for 32 tiles instead of ~36 for the row-major order.
 constexpr int kGroupRows = 8;
 
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -76,55 +80,81 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
   tn = within / rows;
 }
 
-// LDS rows are 64 bytes (four 16-byte chunks of K), swizzled with swizzle64.
-__device__ __forceinline__ int swizzle(int r, int c) { return swizzle64(r, c); }
+// LDS rows are 128 bytes (eight 16-byte chunks); chunk c of row r is stored at c ^ f(r) with
+// f(r) = (r & 7) ^ ((r >> 3) & 3). The 16 lanes a ds_read_b128 serves per cycle read rows R..R+15 (R a multiple of
+// 16) at one logical chunk and land on 16 distinct 16-byte slots of a 256-byte bank window. f only sees row bits
+// 0-4, so it is the same for every 32-row MFMA block.
+__device__ __forceinline__ int row_swz(int r) { return (r & 7) ^ ((r >> 3) & 3); }
 
-// Per-lane byte offsets of one wave's stage loads, computed once per tile. Load i of a wave fills LDS block
-// blk = first_blk + i (16 rows x 64 bytes): lane l fills row 16*blk + l/4, physical chunk l%4, from the logical chunk
-// the swizzle stores there. Rows past the tile's valid rows get the descriptor size as base offset, so adding any
-// K offset keeps them out of range (they read as zero).
-template <int COUNT>
-struct StageOffsets {
-  uint32_t off[COUNT];
-  __device__ __forceinline__ void init(uint32_t oob, int64_t ld, int rows_valid, int first_blk, int lane) {
-#pragma unroll
-    for (int i = 0; i < COUNT; ++i) {
-      const int r = (first_blk + i) * 16 + (lane >> 2);
-      const int c = swizzle(r, lane & 3);
-      off[i] = r < rows_valid ? (uint32_t)(r * ld + c * 16) : oob;
-    }
-  }
+// One tile's operand source: buffer descriptors for its q rows and w rows (rows past the matrix, and every row of a
+// tile past the last one, read as zero). Wave-uniform: it lives in scalar registers.
+struct TileSrc {
+  int m0, n0, rows_m, rows_n;
+  uint32_t bytes_q, bytes_w;
+  __amdgpu_buffer_rsrc_t rq, rw;
 };
 
-// Issue one wave's loads of a stage at K offset k0 into `dst` (LDS, wave-uniform). A lane's 16-byte chunk sits at
-// the same K byte of the stage for every load (the swizzle of its row, 16*blk + lane/4, only sees row bits 1-3, i.e.
-// lane bits 3-5). Chunks at or past K read as zero (the offset moves past the descriptor), branch-free; so does every
-// load of a stage past the end (k0 >= K).
-template <int COUNT>
-__device__ __forceinline__ void load_stage(__amdgpu_buffer_rsrc_t rsrc, const StageOffsets<COUNT>& so, uint32_t oob,
-                                           int k0, int K, unsigned char HF_LDS* dst, int first_blk, int lane) {
-  const int kb = k0 + (swizzle(lane >> 2, lane & 3) << 4);
-  const uint32_t kadd = kb < K ? (uint32_t)k0 : oob;
-#pragma unroll
-  for (int i = 0; i < COUNT; ++i) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + (first_blk + i) * 1024), 16, so.off[i] + kadd,
-                                             0, 0, 0);
-  }
+__device__ __forceinline__ void tile_src(const GemmArgs& a, int id, TileSrc& t) {
+  int tm = 0, tn = 0;
+  const bool live = id < a.tiles_m * a.tiles_n;
+  if (live) tile_of(id, a.tiles_m, a.tiles_n, tm, tn);
+  t.m0 = tm * GBM;
+  t.n0 = tn * GBN;
+  t.rows_m = live ? min(GBM, a.M - t.m0) : 0;
+  t.rows_n = live ? min(GBN, a.N - t.n0) : 0;
+  t.bytes_q = (uint32_t)(t.rows_m * a.ldq);
+  t.bytes_w = (uint32_t)(t.rows_n * a.ldw);
+  t.rq = make_rsrc(a.q + (int64_t)t.m0 * a.ldq, t.bytes_q);
+  t.rw = make_rsrc(a.w + (int64_t)t.n0 * a.ldw, t.bytes_w);
 }
 
-// The low-rank operands of a tile (u rows m or up rows n, rank r <= 64, as 128-byte rows of 8 chunks of 8 bf16,
-// swizzled with swizzle128) are loaded into a free ring slot: 256 rows x 128 bytes = 32 loads of
-// 1 KiB, 4 per wave. Rows past the tile's valid rows and chunks past r read as zero.
-__device__ __forceinline__ void load_lowrank_rows(__amdgpu_buffer_rsrc_t rsrc, uint32_t oob, int64_t ld_bytes,
-                                                  int rows_valid, int r, unsigned char HF_LDS* dst, int wave,
-                                                  int lane) {
+// The per-lane part of a stage load's address, the same for every tile. Load i (0..3) of a wave fills the 1 KiB
+// block blk = 4 * wave + i of its operand (8 rows): lane l fills row r = 8 * blk + l / 8, physical chunk l % 8, from
+// logical chunk (l % 8) ^ f(r) = (l % 8) ^ (l / 8) ^ i (f sees r % 8 = l / 8 and (r / 8) % 4 = i).
+struct LaneLoad {
+  uint32_t row_q, row_w;  // (l / 8) * ld of q and of w
+  uint32_t chunk;         // ((l % 8) ^ (l / 8)) * 16
+  int lrow;               // l / 8
+};
+
+// Load j (0..7) of this wave's share of stage kt, into slot `slot`: j < 4 fills q block 4 * wave + j, j >= 4 fills
+// w block 4 * wave + j - 4. Rows past the tile's valid rows and chunks at or past K read as zero (the offset moves
+// past the descriptor), branch-free; so does every load of a stage past the end.
+__device__ __forceinline__ void load_one(const GemmArgs& a, const TileSrc& t, const LaneLoad& ll, int kt, int j,
+                                         unsigned char HF_LDS* slot, int wave) {
+  const int i = j & 3;
+  const bool isw = j >= 4;
+  const int64_t ld = isw ? a.ldw : a.ldq;
+  const int rows_valid = isw ? t.rows_n : t.rows_m;
+  const uint32_t oob = isw ? t.bytes_w : t.bytes_q;
+  const int row = 32 * wave + 8 * i + ll.lrow;
+  const uint32_t cb = ll.chunk ^ (uint32_t)(16 * i);
+  const uint32_t k0 = (uint32_t)(kt * GBK);
+  const uint32_t off = (isw ? ll.row_w : ll.row_q) + (uint32_t)((32 * wave + 8 * i) * ld) + cb + k0;
+  const uint32_t voff = ((row < rows_valid) & (k0 + cb < (uint32_t)a.K)) ? off : oob;  // '&': no branch
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(isw ? t.rw : t.rq,
+                                           (void HF_LDS*)(slot + (isw ? kAStage : 0) + (4 * wave + i) * 1024), 16,
+                                           voff, 0, 0, 0);
+}
+
+// The low-rank operands of a tile (u rows m into the slot's q half, up rows n into its w half, rank r <= 64: one
+// 128-byte row each; chunks past r and rows past the tile's valid rows read as zero), in the same 8 loads per wave
+// as a stage.
+__device__ __forceinline__ void load_lowrank(const GemmArgs& a, const TileSrc& t, unsigned char HF_LDS* slot,
+                                             int wave, int lane) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int blk = wave * 4 + i;
-    const int row = blk * 8 + (lane >> 3);
-    const int c = swizzle128(row, lane & 7);
-    const uint32_t voff = (row < rows_valid && c * 8 < r) ? (uint32_t)(row * ld_bytes + c * 16) : oob;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + blk * 1024), 16, voff, 0, 0, 0);
+  for (int j = 0; j < 8; ++j) {
+    const bool isup = j >= 4;
+    const int64_t ld_bytes = (isup ? a.ldup : a.ldu) * 2;
+    const int rows_valid = isup ? t.rows_n : t.rows_m;
+    const uint32_t bytes = (uint32_t)(rows_valid * ld_bytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(
+        isup ? (const void*)(a.up + (int64_t)t.n0 * a.ldup) : (const void*)(a.u + (int64_t)t.m0 * a.ldu), bytes);
+    const int blk = 4 * wave + (j & 3), r = 8 * blk + (lane >> 3);
+    const int c = (lane & 7) ^ row_swz(r);
+    const uint32_t voff = ((r < rows_valid) & (c * 8 < a.r)) ? (uint32_t)(r * ld_bytes + c * 16) : bytes;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void HF_LDS*)(slot + (isup ? kAStage : 0) + blk * 1024), 16,
+                                             voff, 0, 0, 0);
   }
 }
 
@@ -133,15 +163,16 @@ struct Frags {
   v4i b[2];  // weight rows: 2 blocks of 32 (the wave's 64 n)
 };
 
-__device__ __forceinline__ void read_frags(Frags& f, const unsigned char HF_LDS* stage, int wm, int wn, int ks,
-                                           int sub, int half) {
-  const int chunk = swizzle(sub, 2 * ks + half) * 16;  // blocks start at multiples of 32 rows: f(row) == f(sub)
-  const unsigned char HF_LDS* As = stage;
-  const unsigned char HF_LDS* Bs = stage + kAStage;
+// Operand fragments of K step ks (32 bytes: chunks 2ks and 2ks + 1; lane half h reads chunk 2ks + h of row sub of
+// each 32-row block). `ca` is this lane's byte offset of that chunk within its row block (sub * 128 + swizzled
+// chunk); the block and slot offsets are wave-uniform.
+__device__ __forceinline__ void read_frags(Frags& f, const unsigned char HF_LDS* slot, int wm, int wn, int ca) {
+  const unsigned char HF_LDS* As = slot + wm * 128 * GBK + ca;
+  const unsigned char HF_LDS* Bs = slot + kAStage + wn * 64 * GBK + ca;
 #pragma unroll
-  for (int jb = 0; jb < 4; ++jb) f.a[jb] = *(const v4i HF_LDS*)(As + (wm * 128 + jb * 32 + sub) * GBK + chunk);
+  for (int jb = 0; jb < 4; ++jb) f.a[jb] = *(const v4i HF_LDS*)(As + jb * 32 * GBK);
 #pragma unroll
-  for (int ib = 0; ib < 2; ++ib) f.b[ib] = *(const v4i HF_LDS*)(Bs + (wn * 64 + ib * 32 + sub) * GBK + chunk);
+  for (int ib = 0; ib < 2; ++ib) f.b[ib] = *(const v4i HF_LDS*)(Bs + ib * 32 * GBK);
 }
 
 __device__ __forceinline__ void mma(v16i (&acc)[2][4], const Frags& f) {
@@ -154,63 +185,25 @@ __device__ __forceinline__ void mma(v16i (&acc)[2][4], const Frags& f) {
 
 #define HF_BARRIER() asm volatile("s_barrier" ::: "memory")
 
-// s_waitcnt vmcnt(n) for the wave-uniform counts the persistent loop uses (an unlisted count waits for everything,
-// which is always safe). The loop's accounting relies on vector memory operations completing in issue order (loads,
-// LDS-DMA loads and stores share one in-order counter on gfx9).
+// s_waitcnt vmcnt(n) for the wave-uniform counts the loop uses (an unlisted count waits for everything, which is
+// always safe). The accounting relies on vector memory operations completing in issue order (loads, LDS-DMA loads
+// and stores share one in-order counter on gfx9).
 __device__ __forceinline__ void wait_vm(int n) {
   switch (n) {
     case 8: asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory"); break;
-    case 10: asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)" ::: "memory"); break;
-    case 12: asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)" ::: "memory"); break;
-    case 26: asm volatile("s_waitcnt vmcnt(26) lgkmcnt(0)" ::: "memory"); break;
-    case 28: asm volatile("s_waitcnt vmcnt(28) lgkmcnt(0)" ::: "memory"); break;
+    case 24: asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)" ::: "memory"); break;
     case 40: asm volatile("s_waitcnt vmcnt(40) lgkmcnt(0)" ::: "memory"); break;
-    case 44: asm volatile("s_waitcnt vmcnt(44) lgkmcnt(0)" ::: "memory"); break;
     default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); break;
   }
-}
-
-// One output tile's operand source: the q rows m0.. and w rows n0.. as buffer descriptors (rows past the matrix and
-// every row of a tile past the last one read as zero) and the per-lane stage offsets.
-struct TileSrc {
-  int m0, n0, rows_m, rows_n;
-  uint32_t bytes_q, bytes_w;
-  __amdgpu_buffer_rsrc_t rq, rw;
-  StageOffsets<2> offq, offw;
-};
-
-__device__ __forceinline__ void tile_src(const GemmArgs& a, int id, int wave, int lane, TileSrc& t) {
-  int tm = 0, tn = 0;
-  const bool live = id < a.tiles_m * a.tiles_n;
-  if (live) tile_of(id, a.tiles_m, a.tiles_n, tm, tn);
-  t.m0 = tm * GBM;
-  t.n0 = tn * GBN;
-  t.rows_m = live ? min(GBM, a.M - t.m0) : 0;
-  t.rows_n = live ? min(GBN, a.N - t.n0) : 0;
-  t.bytes_q = (uint32_t)(t.rows_m * a.ldq);
-  t.bytes_w = (uint32_t)(t.rows_n * a.ldw);
-  t.rq = make_rsrc(a.q + (int64_t)t.m0 * a.ldq, t.bytes_q);
-  t.rw = make_rsrc(a.w + (int64_t)t.n0 * a.ldw, t.bytes_w);
-  t.offq.init(t.bytes_q, a.ldq, t.rows_m, wave * 2, lane);
-  t.offw.init(t.bytes_w, a.ldw, t.rows_n, wave * 2, lane);
-}
-
-// Stage kt of tile t into ring slot `slot`: 4 loads per wave (2 of q, 2 of w).
-__device__ __forceinline__ void load_tile_stage(const TileSrc& t, const GemmArgs& a, int kt,
-                                                unsigned char HF_LDS* slot, int wave, int lane) {
-  load_stage<2>(t.rq, t.offq, t.bytes_q, kt * GBK, a.K, slot, wave * 2, lane);
-  load_stage<2>(t.rw, t.offw, t.bytes_w, kt * GBK, a.K, slot + kAStage, wave * 2, lane);
 }
 
 // Output modes: int32 accumulators; bf16 with the dequantization (and, for r > 64, the low-rank term from global
 // memory) and bias; bf16 with a rank <= 64 low-rank term whose operands ride the ring.
 constexpr int kOutI32 = 0, kOutBf16 = 1, kOutBf16Lr = 2;
 
-// Persistent kernel: one workgroup per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... The ring of 4 stages
-// runs continuously across tiles: the last 4 iterations of a tile refill their slots with the next tile's first
-// stages (after the tile's u and up tiles in low-rank mode), so a tile starts with its operands in flight and the
-// epilogue's output stores drain while the next tile computes. Every ring step issues exactly 4 loads per wave
-// (past the last tile they read zeros), which keeps every wait a fixed vmcnt.
+
+// Persistent kernel: one workgroup per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... Every wave issues the
+// same number of memory operations in the same order, so every wait is a constant vmcnt.
 template <int OUT>
 __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[];
@@ -220,43 +213,79 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   const int wm = wave & 1, wn = wave >> 1;  // 2 (m) x 4 (n) waves of 128 x 64
   const int sub = lane & 31, half = lane >> 5;
   constexpr bool kLr = OUT == kOutBf16Lr;
-  constexpr int kParamLoads = OUT == kOutI32 ? 0 : 2;  // per thread and tile
   constexpr int kFastStores = OUT == kOutI32 ? 32 : 16;  // per wave and tile, full tiles only
   float HF_LDS* params = (float HF_LDS*)(smem + kRingBytes);
   const int pt = threadIdx.x & 255;
-  auto slot_at = [&](int step) { return smem + (step & (kStages - 1)) * kStageBytes; };
+  auto slot_at = [&](int s) { return smem + (s & 1) * kSlotBytes; };
 
-  // K steps per tile, at least 7 so the three first steps, the steady loop and the four refill steps never overlap
-  // (stages past K read zeros and add nothing).
-  const int nk = max((a.K + GBK - 1) / GBK, kStages + 3);
+  // This lane's fragment offsets for the four K steps of a stage.
+  int ca[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) ca[ks] = sub * GBK + (((2 * ks + half) ^ row_swz(sub)) << 4);
+
+  // K stages per tile, at least 2 (stages past K read zeros and add nothing).
+  const int nk = max((a.K + GBK - 1) / GBK, 2);
   const int total = a.tiles_m * a.tiles_n;
   int id = blockIdx.x;
+  LaneLoad ll;
+  ll.lrow = lane >> 3;
+  ll.row_q = (uint32_t)((lane >> 3) * a.ldq);
+  ll.row_w = (uint32_t)((lane >> 3) * a.ldw);
+  ll.chunk = (uint32_t)(((lane & 7) ^ (lane >> 3)) << 4);
   TileSrc cur;
-  tile_src(a, id, wave, lane, cur);
+  tile_src(a, id, cur);
 #pragma unroll
-  for (int j = 0; j < kStages; ++j) load_tile_stage(cur, a, j, slot_at(j), wave, lane);
+  for (int j = 0; j < kStageLoads; ++j) load_one(a, cur, ll, 0, j, slot_at(0), wave);
+#pragma unroll
+  for (int j = 0; j < kStageLoads; ++j) load_one(a, cur, ll, 1, j, slot_at(1), wave);
 
-  int g = 0;             // ring step of the current tile's stage 0
-  bool stores_behind = false;  // the previous tile's epilogue left kFastStores stores behind its stage 3
+  int g = 0;  // slot parity of the current tile's stage 0
   Frags f0, f1;
   v16i acc[2][4];
 
-  // One tile; SPILL counts the stores the previous epilogue issued after this tile's stage 3 (they precede the
-  // parameter loads), so every wait count below is a constant.
+  // MFMAs of one K step on `use` with the LDS reads of the next fragments (`read`) spread between them, and, when
+  // `loads` issues 8 stage loads, those between the last MFMAs.
+  auto kstep = [&](const Frags& use, auto&& read, auto&& loads) {
+    read();
+    mma(acc, use);
+    loads();
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM (stage loads)
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto nothing = [] {};
+
+  // One tile. SPILL is the number of the previous epilogue's stores that sit between this tile's stage 0 and stage
+  // 1 loads (0 when they were drained), so every wait count below is a constant.
   auto tile = [&](auto spill_tag) -> bool {
     constexpr int spill = decltype(spill_tag)::value;
-    const int next_id = id + gridDim.x;
-    TileSrc nxt;
-    tile_src(a, next_id, wave, lane, nxt);
+    // An opaque copy of the wave id for this tile's load addressing: keeps the compiler from hoisting the
+    // per-load scalar offsets out of the tile loop (they would stay live, and spill, across it).
+    int wv = wave;
+    asm volatile("" : "+s"(wv));
 
-    // Stage 0 landed (stages 1..3 and the previous tile's stores may still be in flight).
-    wait_vm(12 + spill);
+    // Stage 0 has landed for this wave once only the stores and stage 1's loads remain; the barrier makes it so for
+    // every wave.
+    wait_vm(spill + kStageLoads);
     HF_BARRIER();
-    read_frags(f0, slot_at(g), wm, wn, 0, sub, half);
+    read_frags(f0, slot_at(g), wm, wn, ca[0]);
 
-    // The epilogue's per-row and per-column factors, loaded now and parked in LDS when the epilogue starts:
-    // threads 0..255 take sx of row m0 + t and wscale of column n0 + t, threads 256..511 the bias of column
-    // n0 + t - 256 (and a second, unused load so every wave issues the same count). Clamped, branch-free.
+    // The epilogue's per-row and per-column factors, loaded now (every wave issues two loads) and parked in LDS
+    // when the epilogue starts: threads 0..255 take sx of row m0 + t and wscale of column n0 + t, threads 256..511
+    // the bias of column n0 + t - 256. Clamped, branch-free.
     float p_val = 0.0f;
     uint32_t p_bias = 0;
     if (OUT != kOutI32) {
@@ -265,85 +294,68 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       p_val = a.sx[mr];
       p_bias = threadIdx.x < 256 ? __float_as_uint(a.sw[nc]) : (uint32_t)bsrc[nc];
     }
-    constexpr int early = 8 + spill + kParamLoads;  // wait count while those operations sit behind the stage
 
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = (v16i){0};
 
-    // Step kt: read the second K half of slot kt while multiplying the first; wait until stage kt + 1 landed (for
-    // this wave) and the slot's reads returned; barrier; read stage kt + 1's first half, refill slot kt and multiply
-    // the second half, with LDS reads and loads spread between the MFMAs.
-    auto step = [&](int kt, int vm, bool read_next, auto&& refill) {
-      read_frags(f1, slot_at(g + kt), wm, wn, 1, sub, half);
-      mma(acc, f0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
-      __builtin_amdgcn_sched_barrier(0);  // every MFMA of the first half issues before the wait and barrier
-      wait_vm(vm);
+    // Stage s: K steps 0..2, then (unless s is the last stage) wait for stage s + 1, barrier (every wave is done
+    // with slot s), and K step 3 with the reads of stage s + 1's first fragments and the refill of slot s.
+    auto first_steps = [&](int s) {
+      const unsigned char HF_LDS* sl = slot_at(g + s);
+      kstep(f0, [&] { read_frags(f1, sl, wm, wn, ca[1]); }, nothing);
+      kstep(f1, [&] { read_frags(f0, sl, wm, wn, ca[2]); }, nothing);
+      kstep(f0, [&] { read_frags(f1, sl, wm, wn, ca[3]); }, nothing);
+    };
+    auto boundary = [&](int s, auto&& loads) {
+      wait_vm(0);
       HF_BARRIER();
-      __builtin_amdgcn_sched_barrier(0);
-      if (read_next) read_frags(f0, slot_at(g + kt + 1), wm, wn, 0, sub, half);
-      refill(slot_at(g + kt));
-      mma(acc, f1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);  // VMEM (stage load)
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
-      __builtin_amdgcn_sched_barrier(0);
+      if (OUT != kOutI32 && s == 0) {
+        // The parameter loads have landed (vmcnt(0)); park them in LDS for the epilogue. Nothing reads this area
+        // until then, and the barriers in between publish it. An absent bias is -0.0, which adds exactly.
+        if (threadIdx.x < 256) {
+          params[pt] = (cur.m0 + pt < a.M) ? p_val : 0.0f;
+          params[256 + pt] = (cur.n0 + pt < a.N) ? __uint_as_float(p_bias) : 0.0f;
+        } else {
+          params[512 + pt] = (cur.n0 + pt < a.N && a.bias) ? __uint_as_float(p_bias << 16) : -0.0f;
+        }
+      }
+      kstep(f1, [&] { read_frags(f0, slot_at(g + s + 1), wm, wn, ca[0]); }, loads);
     };
-    auto own_stage = [&](int kt) {
-      return [&, kt](unsigned char HF_LDS* s) { load_tile_stage(cur, a, kt, s, wave, lane); };
-    };
-    auto next_stage = [&](int kt) {
-      return [&, kt](unsigned char HF_LDS* s) { load_tile_stage(nxt, a, kt, s, wave, lane); };
-    };
-
-    // Steps 0..nk-5 refill with this tile's stages 4..nk-1; the first three still have the stores and parameter
-    // loads behind the stage they wait for.
-    step(0, early, true, own_stage(kStages));
-    step(1, early, true, own_stage(kStages + 1));
-    step(2, early, true, own_stage(kStages + 2));
-    int kt = 3;
-    for (; kt < nk - kStages; ++kt) step(kt, 8, true, own_stage(kt + kStages));
-    // The last four steps refill with the tile's low-rank operands and the next tile's first stages.
-    const __amdgpu_buffer_rsrc_t ru =
-        make_rsrc(a.u + (int64_t)cur.m0 * a.ldu, kLr ? (uint32_t)(cur.rows_m * a.ldu * 2) : 0u);
-    const __amdgpu_buffer_rsrc_t rup =
-        make_rsrc(a.up + (int64_t)cur.n0 * a.ldup, kLr ? (uint32_t)(cur.rows_n * a.ldup * 2) : 0u);
-    if constexpr (kLr) {
-      step(kt, 8, true, [&](unsigned char HF_LDS* s) {
-        load_lowrank_rows(ru, (uint32_t)(cur.rows_m * a.ldu * 2), a.ldu * 2, cur.rows_m, a.r, s, wave, lane);
+    int s = 0;
+    for (; s < nk - 2; ++s) {
+      first_steps(s);
+      boundary(s, [&] {
+#pragma unroll
+        for (int j = 0; j < kStageLoads; ++j) load_one(a, cur, ll, s + 2, j, slot_at(g + s), wv);
       });
-      step(kt + 1, 8, true, [&](unsigned char HF_LDS* s) {
-        load_lowrank_rows(rup, (uint32_t)(cur.rows_n * a.ldup * 2), a.ldup * 2, cur.rows_n, a.r, s, wave, lane);
-      });
-      step(kt + 2, 8, true, next_stage(0));
-      step(kt + 3, 8, false, next_stage(1));
-    } else {
-      step(kt, 8, true, next_stage(0));
-      step(kt + 1, 8, true, next_stage(1));
-      step(kt + 2, 8, true, next_stage(2));
-      step(kt + 3, 8, false, next_stage(3));
     }
+    // Stage nk - 2 refills its slot with the next tile's stage 0; stage nk - 1 has no successor.
+    const int next_id = id + gridDim.x;
+    TileSrc nxt;
+    tile_src(a, next_id, nxt);
+    first_steps(s);
+    boundary(s, [&] {
+#pragma unroll
+      for (int j = 0; j < kStageLoads; ++j) load_one(a, nxt, ll, 0, j, slot_at(g + s), wv);
+    });
+    first_steps(s + 1);
+    kstep(f1, nothing, nothing);
 
     // ------------------------------------------------------------------------------------------------ epilogue
+    // Every wave is done with the last stage's slot, the epilogue slot E: in low-rank mode it receives the tile's
+    // low-rank operands, which land while the accumulators are dequantized; then it stages the output.
+    unsigned char HF_LDS* eslot = slot_at(g + nk - 1);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    HF_BARRIER();
+    if constexpr (kLr) load_lowrank(a, cur, eslot, wv, lane);
+
+    // Per-lane epilogue indices from an opaque copy of the lane id: keeps the compiler from hoisting their address
+    // arithmetic out of the tile loop, where it would stay live (and spill) across the main loop.
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    const int esub = el & 31, ehalf = el >> 5;
     // Output layout of a 32x32 block: lane holds column j = lane % 32 (the row m here) and, in register v, row
     // i = 8*(v/4) + 4*(lane/32) + v%4 (the column n here): four consecutive n per group of four registers.
     const int m0 = cur.m0, n0 = cur.n0;
@@ -353,12 +365,12 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       int32_t* out = static_cast<int32_t*>(a.out);
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
-        const int m = m0 + wm * 128 + jb * 32 + sub;
+        const int m = m0 + wm * 128 + jb * 32 + esub;
 #pragma unroll
         for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq) {
-            const int n = n0 + wn * 64 + ib * 32 + 8 * gq + 4 * half;
+            const int n = n0 + wn * 64 + ib * 32 + 8 * gq + 4 * ehalf;
             int32_t* dst = out + (int64_t)m * a.ldo + n;
             const v16i& c = acc[ib][jb];
             if (full) {
@@ -371,25 +383,11 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       }
     } else {
       full = cur.rows_m == GBM && cur.rows_n == GBN && a.out_vec16 && (kLr || a.r == 0);
-      if (threadIdx.x < 256) {
-        params[pt] = (m0 + pt < a.M) ? p_val : 0.0f;
-        params[256 + pt] = (n0 + pt < a.N) ? __uint_as_float(p_bias) : 0.0f;
-      } else {
-        params[512 + pt] = (n0 + pt < a.N && a.bias) ? __uint_as_float(p_bias << 16) : 0.0f;
-      }
-      // Low-rank mode: the up tile (step g + nk + 1) has landed once only the next tile's stages 0 and 1 are
-      // behind it. The barrier also publishes the parameters.
-      if constexpr (kLr) {
-        wait_vm(8);
-      } else {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      }
-      HF_BARRIER();
       float sxv[4];
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb) sxv[jb] = params[wm * 128 + jb * 32 + sub];
-      const unsigned char HF_LDS* u_lds = slot_at(g + nk);
-      const unsigned char HF_LDS* up_lds = slot_at(g + nk + 1);
+      for (int jb = 0; jb < 4; ++jb) sxv[jb] = params[wm * 128 + jb * 32 + esub];
+      const unsigned char HF_LDS* u_lds = eslot;             // u rows m (128-byte rows)
+      const unsigned char HF_LDS* up_lds = eslot + kAStage;  // up rows n
       v16f c[2][4];
 #pragma unroll
       for (int ib = 0; ib < 2; ++ib) {
@@ -397,33 +395,41 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
-            const int nl = wn * 64 + ib * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            const int nl = wn * 64 + ib * 32 + 8 * (v >> 2) + 4 * ehalf + (v & 3);
             c[ib][jb][v] = ((float)acc[ib][jb][v] * sxv[jb]) * params[256 + nl];
           }
+      }
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
         if constexpr (kLr) {
-          // Low-rank term from the LDS tiles (rows of 128 bytes, swizzle128): first operand
-          // up[n, :], second u[m, :], 16 ranks per MFMA, accumulated onto the dequantized values.
-          const int nl = wn * 64 + ib * 32 + sub;
+          // Low-rank term: first operand up[n, :], second u[m, :], 16 ranks per MFMA, accumulated onto the
+          // dequantized values. The operands have landed once nothing is in flight; the barrier makes that true for
+          // every wave's loads.
+          if (ib == 0) {
+            wait_vm(0);
+            HF_BARRIER();
+          }
+          const int nl = wn * 64 + ib * 32 + esub;
           for (int kk = 0; kk < a.r; kk += 16) {
-            const int chunk = kk / 8 + half;
-            const v8bf pf = *(const v8bf HF_LDS*)(up_lds + nl * 128 + swizzle128(nl, chunk) * 16);
+            const int chunk = kk / 8 + ehalf;
+            const v8bf pf = *(const v8bf HF_LDS*)(up_lds + nl * GBK + ((chunk ^ row_swz(nl)) << 4));
 #pragma unroll
             for (int jb = 0; jb < 4; ++jb) {
-              const int ml = wm * 128 + jb * 32 + sub;
-              const v8bf uf = *(const v8bf HF_LDS*)(u_lds + ml * 128 + swizzle128(ml, chunk) * 16);
+              const int ml = wm * 128 + jb * 32 + esub;
+              const v8bf uf = *(const v8bf HF_LDS*)(u_lds + ml * GBK + ((chunk ^ row_swz(ml)) << 4));
               c[ib][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[ib][jb], 0, 0, 0);
             }
           }
         } else if (a.r > 0) {
           // Ranks above 64: the same product from global memory.
-          const int nrow = min(n0 + wn * 64 + ib * 32 + sub, a.N - 1);
+          const int nrow = min(n0 + wn * 64 + ib * 32 + esub, a.N - 1);
           for (int kk = 0; kk < a.r; kk += 16) {
-            const int k = kk + 8 * half;
+            const int k = kk + 8 * ehalf;
             const v8bf pf =
                 (k < a.r) ? *reinterpret_cast<const v8bf*>(a.up + (int64_t)nrow * a.ldup + k) : (v8bf){0};
 #pragma unroll
             for (int jb = 0; jb < 4; ++jb) {
-              const int mrow = min(m0 + wm * 128 + jb * 32 + sub, a.M - 1);
+              const int mrow = min(m0 + wm * 128 + jb * 32 + esub, a.M - 1);
               const v8bf uf =
                   (k < a.r) ? *reinterpret_cast<const v8bf*>(a.u + (int64_t)mrow * a.ldu + k) : (v8bf){0};
               c[ib][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[ib][jb], 0, 0, 0);
@@ -431,66 +437,90 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
           }
         }
       }
+      // Every wave is done with the low-rank operands: the epilogue slot stages the output, 8 KiB per wave (64 rows
+      // of 128 bytes, swizzled like the operands), in two rounds of two row blocks. Each lane then reads back 16
+      // bytes of each of 8 rows and each store instruction writes 8 whole rows.
       if constexpr (kLr) {
-        // Every wave is done with the u and up slots: refill them with the next tile's stages 2 and 3.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         HF_BARRIER();
-        load_tile_stage(nxt, a, 2, slot_at(g + nk), wave, lane);
-        load_tile_stage(nxt, a, 3, slot_at(g + nk + 1), wave, lane);
       }
-      // Bias, bf16, and the stores: after one exchange between the lane halves (v_permlane32_swap: lanes 32..63 of
-      // the first operand <-> lanes 0..31 of the second), lane (sub, h) holds columns 16h..16h+15 of row sub of
-      // the block, 32 contiguous bytes written as two 16-byte stores; the two halves cover the row's 64 bytes.
+      unsigned char HF_LDS* stage_out = eslot + wave * 8192;
       uint16_t* out = static_cast<uint16_t*>(a.out);
-      const bool has_bias = a.bias != nullptr;
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
+      for (int rd = 0; rd < 2; ++rd) {
 #pragma unroll
-        for (int jb = 0; jb < 4; ++jb) {
-          uint32_t pk[4][2];
+        for (int jj = 0; jj < 2; ++jj) {
+          const int jb = 2 * rd + jj;
+          const int row = jj * 32 + esub;
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            float v[4];
+          for (int ib = 0; ib < 2; ++ib) {
+            // Bias and bf16. After one exchange between the lane halves (v_permlane32_swap: lanes 32..63 of the
+            // first operand <-> lanes 0..31 of the second), lane (sub, h) holds columns 16h..16h+15 of row sub of
+            // the block: 16-byte chunk 4ib + 2h of the wave's 128-byte output row in w4[0], w4[2] and chunk
+            // 4ib + 2h + 1 in w4[1], w4[3].
+            uint32_t w4[4][2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              v[e] = c[ib][jb][4 * gq + e];
-              if (has_bias) v[e] = v[e] + params[512 + wn * 64 + ib * 32 + 8 * gq + 4 * half + e];
+            for (int gq = 0; gq < 4; ++gq) {
+              float v[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                v[e] = c[ib][jb][4 * gq + e];
+                v[e] = v[e] + params[512 + wn * 64 + ib * 32 + 8 * gq + 4 * ehalf + e];
+              }
+              w4[gq][0] = pack_bf16x2(v[0], v[1]);
+              w4[gq][1] = pack_bf16x2(v[2], v[3]);
             }
-            pk[gq][0] = pack_bf16x2(v[0], v[1]);
-            pk[gq][1] = pack_bf16x2(v[2], v[3]);
-          }
 #pragma unroll
-          for (int w = 0; w < 2; ++w) {
-            const auto s02 = __builtin_amdgcn_permlane32_swap(pk[0][w], pk[2][w], false, false);
-            const auto s13 = __builtin_amdgcn_permlane32_swap(pk[1][w], pk[3][w], false, false);
-            pk[0][w] = s02[0];
-            pk[2][w] = s02[1];
-            pk[1][w] = s13[0];
-            pk[3][w] = s13[1];
-          }
-          const int m = m0 + wm * 128 + jb * 32 + sub;
-          const int n = n0 + wn * 64 + ib * 32 + 16 * half;
-          uint16_t* dst = out + (int64_t)m * a.ldo + n;
-          const v4i lo = (v4i){(int)pk[0][0], (int)pk[0][1], (int)pk[2][0], (int)pk[2][1]};
-          const v4i hi = (v4i){(int)pk[1][0], (int)pk[1][1], (int)pk[3][0], (int)pk[3][1]};
-          if (full) {
-            *reinterpret_cast<v4i*>(dst) = lo;
-            *reinterpret_cast<v4i*>(dst + 8) = hi;
-          } else if (m < a.M) {
-            const uint32_t wds[8] = {pk[0][0], pk[0][1], pk[2][0], pk[2][1], pk[1][0], pk[1][1], pk[3][0], pk[3][1]};
-            for (int e = 0; e < 16; ++e)
-              if (n + e < a.N) dst[e] = (uint16_t)(wds[e >> 1] >> (16 * (e & 1)));
+            for (int w = 0; w < 2; ++w) {
+              const auto s02 = __builtin_amdgcn_permlane32_swap(w4[0][w], w4[2][w], false, false);
+              const auto s13 = __builtin_amdgcn_permlane32_swap(w4[1][w], w4[3][w], false, false);
+              w4[0][w] = s02[0];
+              w4[2][w] = s02[1];
+              w4[1][w] = s13[0];
+              w4[3][w] = s13[1];
+            }
+            const int c0 = 4 * ib + 2 * ehalf;
+            *(v4i HF_LDS*)(stage_out + row * GBK + ((c0 ^ row_swz(row)) << 4)) =
+                (v4i){(int)w4[0][0], (int)w4[0][1], (int)w4[2][0], (int)w4[2][1]};
+            *(v4i HF_LDS*)(stage_out + row * GBK + (((c0 + 1) ^ row_swz(row)) << 4)) =
+                (v4i){(int)w4[1][0], (int)w4[1][1], (int)w4[3][0], (int)w4[3][1]};
           }
         }
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int row = 8 * i + (el >> 3), ch = el & 7;
+          const v4i val = *(const v4i HF_LDS*)(stage_out + row * GBK + ((ch ^ row_swz(row)) << 4));
+          const int m = m0 + wm * 128 + 64 * rd + row;
+          const int n = n0 + wn * 64 + 8 * ch;
+          uint16_t* dst = out + (int64_t)m * a.ldo + n;
+          if (full) {
+            *reinterpret_cast<v4i*>(dst) = val;
+          } else if (m < a.M) {
+            if (a.out_vec16 && n + 8 <= a.N) {
+              *reinterpret_cast<v4i*>(dst) = val;
+            } else {
+              for (int e = 0; e < 8; ++e)
+                if (n + e < a.N) dst[e] = (uint16_t)((uint32_t)val[e >> 1] >> (16 * (e & 1)));
+            }
+          }
+        }
+        wave_lds_sync();  // the next round rewrites this wave's staging area
       }
     }
     // A partial tile's guarded stores (and the r > 64 global reads) are not a fixed count: drain everything.
     if (!full) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    g += nk + (kLr ? 2 : 0);
+    // Every wave is done with the epilogue slot: it receives the next tile's stage 1.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    HF_BARRIER();
+#pragma unroll
+    for (int j = 0; j < kStageLoads; ++j) load_one(a, nxt, ll, 1, j, eslot, wv);
+    g += nk - 2;
     id = next_id;
     cur = nxt;
     return full;
   };
+  bool stores_behind = false;  // the previous tile's epilogue left kFastStores stores behind the next stage 0
   while (id < total) {
     stores_behind = stores_behind ? tile(std::integral_constant<int, kFastStores>{})
                                   : tile(std::integral_constant<int, 0>{});
