@@ -41,9 +41,17 @@ constexpr int kSlotBytes = kAStage + kBStage;     // 64 KiB
 constexpr int kRingBytes = 2 * kSlotBytes;        // 128 KiB
 constexpr int kParamBytes = 3 * 256 * 4;          // the tile's sx, wscale and bias (fp32)
 constexpr int kGemmLds = kRingBytes + kParamBytes;
-constexpr int kWaves = 8;                         // 2 per SIMD: one wave's barrier wait hides under the other's MFMAs
+#ifndef HF_GEMM_WAVES
+#define HF_GEMM_WAVES 8
+#endif
+// Waves per workgroup: 8 = 2 (m) x 4 (n) waves of 128 x 64 (two per SIMD), 4 = 2 x 2 waves of 128 x 128 (one per
+// SIMD, accumulators in AGPRs, a third fewer LDS fragment reads per MFMA).
+constexpr int kWaves = HF_GEMM_WAVES;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kStageLoads = 8;                    // load instructions per wave per stage (4 of q, 4 of w)
+constexpr int WN = 2 * GBN / kWaves;              // n columns per wave
+constexpr int NB = WN / 32;                       // 32-column MFMA blocks per wave
+constexpr int kBlkPerWave = 32 / kWaves;          // 1 KiB load blocks per operand per wave and stage
+constexpr int kStageLoads = 2 * kBlkPerWave;      // load instructions per wave per stage
 
 struct GemmArgs {
   const int8_t* q;
@@ -108,49 +116,50 @@ __device__ __forceinline__ void tile_src(const GemmArgs& a, int id, TileSrc& t) 
   t.rw = make_rsrc(a.w + (int64_t)t.n0 * a.ldw, t.bytes_w);
 }
 
-// The per-lane part of a stage load's address, the same for every tile. Load i (0..3) of a wave fills the 1 KiB
-// block blk = 4 * wave + i of its operand (8 rows): lane l fills row r = 8 * blk + l / 8, physical chunk l % 8, from
-// logical chunk (l % 8) ^ f(r) = (l % 8) ^ (l / 8) ^ i (f sees r % 8 = l / 8 and (r / 8) % 4 = i).
+// The per-lane part of a stage load's address, the same for every tile. Load i of a wave fills the 1 KiB block
+// blk = kBlkPerWave * wave + i of its operand (8 rows): lane l fills row r = 8 * blk + l / 8, physical chunk l % 8,
+// from logical chunk (l % 8) ^ f(r) = (l % 8) ^ (l / 8) ^ (i % 4) (f sees r % 8 = l / 8 and (r / 8) % 4 = i % 4).
 struct LaneLoad {
   uint32_t row_q, row_w;  // (l / 8) * ld of q and of w
   uint32_t chunk;         // ((l % 8) ^ (l / 8)) * 16
   int lrow;               // l / 8
 };
 
-// Load j (0..7) of this wave's share of stage kt, into slot `slot`: j < 4 fills q block 4 * wave + j, j >= 4 fills
-// w block 4 * wave + j - 4. Rows past the tile's valid rows and chunks at or past K read as zero (the offset moves
+// Load j of this wave's share of stage kt, into slot `slot`: j < kBlkPerWave fills q block kBlkPerWave * wave + j,
+// the others w block kBlkPerWave * wave + j - kBlkPerWave. Rows past the tile's valid rows and chunks at or past K read as zero (the offset moves
 // past the descriptor), branch-free; so does every load of a stage past the end.
 __device__ __forceinline__ void load_one(const GemmArgs& a, const TileSrc& t, const LaneLoad& ll, int kt, int j,
                                          unsigned char HF_LDS* slot, int wave) {
-  const int i = j & 3;
-  const bool isw = j >= 4;
+  const int i = j % kBlkPerWave;
+  const bool isw = j >= kBlkPerWave;
   const int64_t ld = isw ? a.ldw : a.ldq;
   const int rows_valid = isw ? t.rows_n : t.rows_m;
   const uint32_t oob = isw ? t.bytes_w : t.bytes_q;
-  const int row = 32 * wave + 8 * i + ll.lrow;
-  const uint32_t cb = ll.chunk ^ (uint32_t)(16 * i);
+  const int row0 = 8 * (kBlkPerWave * wave + i);
+  const int row = row0 + ll.lrow;
+  const uint32_t cb = ll.chunk ^ (uint32_t)(16 * (i & 3));
   const uint32_t k0 = (uint32_t)(kt * GBK);
-  const uint32_t off = (isw ? ll.row_w : ll.row_q) + (uint32_t)((32 * wave + 8 * i) * ld) + cb + k0;
+  const uint32_t off = (isw ? ll.row_w : ll.row_q) + (uint32_t)(row0 * ld) + cb + k0;
   const uint32_t voff = ((row < rows_valid) & (k0 + cb < (uint32_t)a.K)) ? off : oob;  // '&': no branch
   __builtin_amdgcn_raw_ptr_buffer_load_lds(isw ? t.rw : t.rq,
-                                           (void HF_LDS*)(slot + (isw ? kAStage : 0) + (4 * wave + i) * 1024), 16,
+                                           (void HF_LDS*)(slot + (isw ? kAStage : 0) + (row0 / 8) * 1024), 16,
                                            voff, 0, 0, 0);
 }
 
 // The low-rank operands of a tile (u rows m into the slot's q half, up rows n into its w half, rank r <= 64: one
-// 128-byte row each; chunks past r and rows past the tile's valid rows read as zero), in the same 8 loads per wave
-// as a stage.
+// 128-byte row each; chunks past r and rows past the tile's valid rows read as zero), in as many loads per wave as
+// a stage.
 __device__ __forceinline__ void load_lowrank(const GemmArgs& a, const TileSrc& t, unsigned char HF_LDS* slot,
                                              int wave, int lane) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const bool isup = j >= 4;
+  for (int j = 0; j < kStageLoads; ++j) {
+    const bool isup = j >= kBlkPerWave;
     const int64_t ld_bytes = (isup ? a.ldup : a.ldu) * 2;
     const int rows_valid = isup ? t.rows_n : t.rows_m;
     const uint32_t bytes = (uint32_t)(rows_valid * ld_bytes);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(
         isup ? (const void*)(a.up + (int64_t)t.n0 * a.ldup) : (const void*)(a.u + (int64_t)t.m0 * a.ldu), bytes);
-    const int blk = 4 * wave + (j & 3), r = 8 * blk + (lane >> 3);
+    const int blk = kBlkPerWave * wave + j % kBlkPerWave, r = 8 * blk + (lane >> 3);
     const int c = (lane & 7) ^ row_swz(r);
     const uint32_t voff = ((r < rows_valid) & (c * 8 < a.r)) ? (uint32_t)(r * ld_bytes + c * 16) : bytes;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void HF_LDS*)(slot + (isup ? kAStage : 0) + blk * 1024), 16,
@@ -159,8 +168,8 @@ __device__ __forceinline__ void load_lowrank(const GemmArgs& a, const TileSrc& t
 }
 
 struct Frags {
-  v4i a[4];  // activation rows: 4 blocks of 32 (the wave's 128 m)
-  v4i b[2];  // weight rows: 2 blocks of 32 (the wave's 64 n)
+  v4i a[4];   // activation rows: 4 blocks of 32 (the wave's 128 m)
+  v4i b[NB];  // weight rows: NB blocks of 32 (the wave's WN n)
 };
 
 // Operand fragments of K step ks (32 bytes: chunks 2ks and 2ks + 1; lane half h reads chunk 2ks + h of row sub of
@@ -168,16 +177,16 @@ struct Frags {
 // chunk); the block and slot offsets are wave-uniform.
 __device__ __forceinline__ void read_frags(Frags& f, const unsigned char HF_LDS* slot, int wm, int wn, int ca) {
   const unsigned char HF_LDS* As = slot + wm * 128 * GBK + ca;
-  const unsigned char HF_LDS* Bs = slot + kAStage + wn * 64 * GBK + ca;
+  const unsigned char HF_LDS* Bs = slot + kAStage + wn * WN * GBK + ca;
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) f.a[jb] = *(const v4i HF_LDS*)(As + jb * 32 * GBK);
 #pragma unroll
-  for (int ib = 0; ib < 2; ++ib) f.b[ib] = *(const v4i HF_LDS*)(Bs + ib * 32 * GBK);
+  for (int ib = 0; ib < NB; ++ib) f.b[ib] = *(const v4i HF_LDS*)(Bs + ib * 32 * GBK);
 }
 
-__device__ __forceinline__ void mma(v16i (&acc)[2][4], const Frags& f) {
+__device__ __forceinline__ void mma(v16i (&acc)[NB][4], const Frags& f) {
 #pragma unroll
-  for (int ib = 0; ib < 2; ++ib)
+  for (int ib = 0; ib < NB; ++ib)
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
       acc[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[ib], f.a[jb], acc[ib][jb], 0, 0, 0);
@@ -191,8 +200,10 @@ __device__ __forceinline__ void mma(v16i (&acc)[2][4], const Frags& f) {
 __device__ __forceinline__ void wait_vm(int n) {
   switch (n) {
     case 8: asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory"); break;
+    case 16: asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)" ::: "memory"); break;
     case 24: asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)" ::: "memory"); break;
     case 40: asm volatile("s_waitcnt vmcnt(40) lgkmcnt(0)" ::: "memory"); break;
+    case 48: asm volatile("s_waitcnt vmcnt(48) lgkmcnt(0)" ::: "memory"); break;
     default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); break;
   }
 }
@@ -210,10 +221,13 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)smem_raw;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps LDS addresses scalar
-  const int wm = wave & 1, wn = wave >> 1;  // 2 (m) x 4 (n) waves of 128 x 64
+  const int wm = wave & 1, wn = wave >> 1;  // 2 (m) x (kWaves / 2) (n) waves of 128 x WN
   const int sub = lane & 31, half = lane >> 5;
   constexpr bool kLr = OUT == kOutBf16Lr;
-  constexpr int kFastStores = OUT == kOutI32 ? 32 : 16;  // per wave and tile, full tiles only
+  // Stores per wave of a full tile, when the wait for the next stage 0 behind them fits the 6-bit wait counter
+  // (else they are drained).
+  constexpr int kTileStores = GBM * GBN * (OUT == kOutI32 ? 4 : 2) / (kWaves * 1024);
+  constexpr int kFastStores = kTileStores + kStageLoads <= 63 ? kTileStores : 0;
   float HF_LDS* params = (float HF_LDS*)(smem + kRingBytes);
   const int pt = threadIdx.x & 255;
   auto slot_at = [&](int s) { return smem + (s & 1) * kSlotBytes; };
@@ -241,29 +255,25 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
 
   int g = 0;  // slot parity of the current tile's stage 0
   Frags f0, f1;
-  v16i acc[2][4];
+  v16i acc[NB][4];
 
-  // MFMAs of one K step on `use` with the LDS reads of the next fragments (`read`) spread between them, and, when
-  // `loads` issues 8 stage loads, those between the last MFMAs.
+  // MFMAs of one K step on `use` with the LDS reads of the next fragments (`read`) spread between them, two per
+  // MFMA, and, when `loads` issues a stage's loads, those two per MFMA after them.
   auto kstep = [&](const Frags& use, auto&& read, auto&& loads) {
     read();
     mma(acc, use);
     loads();
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM (stage loads)
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+    for (int i = 0; i < (4 + NB) / 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+    }
+#pragma unroll
+    for (int i = 0; i < kStageLoads / 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM (stage loads)
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * NB, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
   auto nothing = [] {};
@@ -283,20 +293,23 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     HF_BARRIER();
     read_frags(f0, slot_at(g), wm, wn, ca[0]);
 
-    // The epilogue's per-row and per-column factors, loaded now (every wave issues two loads) and parked in LDS
-    // when the epilogue starts: threads 0..255 take sx of row m0 + t and wscale of column n0 + t, threads 256..511
-    // the bias of column n0 + t - 256. Clamped, branch-free.
-    float p_val = 0.0f;
+    // The epilogue's per-row and per-column factors, loaded now and parked in LDS after the first boundary: thread
+    // t < 256 takes sx of row m0 + t and wscale of column n0 + t, thread 256 + t (with 4 waves: thread t too) the
+    // bias of column n0 + t. Every wave issues the same loads. Clamped, branch-free.
+    float p_val = 0.0f, p_ws = 0.0f;
     uint32_t p_bias = 0;
     if (OUT != kOutI32) {
       const int mr = min(cur.m0 + pt, a.M - 1), nc = min(cur.n0 + pt, a.N - 1);
       const uint16_t* bsrc = a.bias ? a.bias : reinterpret_cast<const uint16_t*>(a.sw);
-      p_val = a.sx[mr];
-      p_bias = threadIdx.x < 256 ? __float_as_uint(a.sw[nc]) : (uint32_t)bsrc[nc];
+      if (kThreads == 256 || threadIdx.x < 256) {
+        p_val = a.sx[mr];
+        p_ws = a.sw[nc];
+      }
+      if (kThreads == 256 || threadIdx.x >= 256) p_bias = (uint32_t)bsrc[nc];
     }
 
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = (v16i){0};
 
@@ -313,12 +326,13 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       HF_BARRIER();
       if (OUT != kOutI32 && s == 0) {
         // The parameter loads have landed (vmcnt(0)); park them in LDS for the epilogue. Nothing reads this area
-        // until then, and the barriers in between publish it. An absent bias is -0.0, which adds exactly.
-        if (threadIdx.x < 256) {
+        // until then, and the barriers in between publish it.
+        if (kThreads == 256 || threadIdx.x < 256) {
           params[pt] = (cur.m0 + pt < a.M) ? p_val : 0.0f;
-          params[256 + pt] = (cur.n0 + pt < a.N) ? __uint_as_float(p_bias) : 0.0f;
-        } else {
-          params[512 + pt] = (cur.n0 + pt < a.N && a.bias) ? __uint_as_float(p_bias << 16) : -0.0f;
+          params[256 + pt] = (cur.n0 + pt < a.N) ? p_ws : 0.0f;
+        }
+        if (kThreads == 256 || threadIdx.x >= 256) {
+          params[512 + pt] = (cur.n0 + pt < a.N) ? __uint_as_float(p_bias << 16) : 0.0f;
         }
       }
       kstep(f1, [&] { read_frags(f0, slot_at(g + s + 1), wm, wn, ca[0]); }, loads);
@@ -367,10 +381,10 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       for (int jb = 0; jb < 4; ++jb) {
         const int m = m0 + wm * 128 + jb * 32 + esub;
 #pragma unroll
-        for (int ib = 0; ib < 2; ++ib)
+        for (int ib = 0; ib < NB; ++ib)
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq) {
-            const int n = n0 + wn * 64 + ib * 32 + 8 * gq + 4 * ehalf;
+            const int n = n0 + wn * WN + ib * 32 + 8 * gq + 4 * ehalf;
             int32_t* dst = out + (int64_t)m * a.ldo + n;
             const v16i& c = acc[ib][jb];
             if (full) {
@@ -388,87 +402,81 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       for (int jb = 0; jb < 4; ++jb) sxv[jb] = params[wm * 128 + jb * 32 + esub];
       const unsigned char HF_LDS* u_lds = eslot;             // u rows m (128-byte rows)
       const unsigned char HF_LDS* up_lds = eslot + kAStage;  // up rows n
-      v16f c[2][4];
+      // Packed bf16 results, two 16-byte chunks per block: pk[ib][jb][0..3] is chunk 4ib + 2h, pk[ib][jb][4..7]
+      // chunk 4ib + 2h + 1 of row esub of block (ib, jb), h = ehalf.
+      uint32_t pk[NB][4][8];
+      const bool has_bias = a.bias != nullptr;
+      // Two column blocks at a time (the fp32 values of two blocks are 128 registers): dequantize, add the low-rank
+      // term, the bias, convert.
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
+      for (int pb = 0; pb < NB; pb += 2) {
+        v16f c[2][4];
 #pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const int ib = pb + i2;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int nl = wn * 64 + ib * 32 + 8 * (v >> 2) + 4 * ehalf + (v & 3);
-            c[ib][jb][v] = ((float)acc[ib][jb][v] * sxv[jb]) * params[256 + nl];
-          }
-      }
+          for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
-        if constexpr (kLr) {
-          // Low-rank term: first operand up[n, :], second u[m, :], 16 ranks per MFMA, accumulated onto the
-          // dequantized values. The operands have landed once nothing is in flight; the barrier makes that true for
-          // every wave's loads.
-          if (ib == 0) {
-            wait_vm(0);
-            HF_BARRIER();
-          }
-          const int nl = wn * 64 + ib * 32 + esub;
-          for (int kk = 0; kk < a.r; kk += 16) {
-            const int chunk = kk / 8 + ehalf;
-            const v8bf pf = *(const v8bf HF_LDS*)(up_lds + nl * GBK + ((chunk ^ row_swz(nl)) << 4));
-#pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-              const int ml = wm * 128 + jb * 32 + esub;
-              const v8bf uf = *(const v8bf HF_LDS*)(u_lds + ml * GBK + ((chunk ^ row_swz(ml)) << 4));
-              c[ib][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[ib][jb], 0, 0, 0);
+            for (int v = 0; v < 16; ++v) {
+              const int nl = wn * WN + ib * 32 + 8 * (v >> 2) + 4 * ehalf + (v & 3);
+              c[i2][jb][v] = ((float)acc[ib][jb][v] * sxv[jb]) * params[256 + nl];
             }
-          }
-        } else if (a.r > 0) {
-          // Ranks above 64: the same product from global memory.
-          const int nrow = min(n0 + wn * 64 + ib * 32 + esub, a.N - 1);
-          for (int kk = 0; kk < a.r; kk += 16) {
-            const int k = kk + 8 * ehalf;
-            const v8bf pf =
-                (k < a.r) ? *reinterpret_cast<const v8bf*>(a.up + (int64_t)nrow * a.ldup + k) : (v8bf){0};
-#pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-              const int mrow = min(m0 + wm * 128 + jb * 32 + esub, a.M - 1);
-              const v8bf uf =
-                  (k < a.r) ? *reinterpret_cast<const v8bf*>(a.u + (int64_t)mrow * a.ldu + k) : (v8bf){0};
-              c[ib][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[ib][jb], 0, 0, 0);
-            }
-          }
         }
-      }
-      // Every wave is done with the low-rank operands: the epilogue slot stages the output, 8 KiB per wave (64 rows
-      // of 128 bytes, swizzled like the operands), in two rounds of two row blocks. Each lane then reads back 16
-      // bytes of each of 8 rows and each store instruction writes 8 whole rows.
-      if constexpr (kLr) {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        HF_BARRIER();
-      }
-      unsigned char HF_LDS* stage_out = eslot + wave * 8192;
-      uint16_t* out = static_cast<uint16_t*>(a.out);
 #pragma unroll
-      for (int rd = 0; rd < 2; ++rd) {
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const int ib = pb + i2;
+          if constexpr (kLr) {
+            // Low-rank term: first operand up[n, :], second u[m, :], 16 ranks per MFMA, accumulated onto the
+            // dequantized values. The operands have landed once nothing is in flight; the barrier makes that true
+            // for every wave's loads.
+            if (pb == 0 && i2 == 0) {
+              wait_vm(0);
+              HF_BARRIER();
+            }
+            const int nl = wn * WN + ib * 32 + esub;
+            for (int kk = 0; kk < a.r; kk += 16) {
+              const int chunk = kk / 8 + ehalf;
+              const v8bf pf = *(const v8bf HF_LDS*)(up_lds + nl * GBK + ((chunk ^ row_swz(nl)) << 4));
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const int jb = 2 * rd + jj;
-          const int row = jj * 32 + esub;
+              for (int jb = 0; jb < 4; ++jb) {
+                const int ml = wm * 128 + jb * 32 + esub;
+                const v8bf uf = *(const v8bf HF_LDS*)(u_lds + ml * GBK + ((chunk ^ row_swz(ml)) << 4));
+                c[i2][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[i2][jb], 0, 0, 0);
+              }
+            }
+          } else if (a.r > 0) {
+            // Ranks above 64: the same product from global memory.
+            const int nrow = min(n0 + wn * WN + ib * 32 + esub, a.N - 1);
+            for (int kk = 0; kk < a.r; kk += 16) {
+              const int k = kk + 8 * ehalf;
+              const v8bf pf =
+                  (k < a.r) ? *reinterpret_cast<const v8bf*>(a.up + (int64_t)nrow * a.ldup + k) : (v8bf){0};
 #pragma unroll
-          for (int ib = 0; ib < 2; ++ib) {
-            // Bias and bf16. After one exchange between the lane halves (v_permlane32_swap: lanes 32..63 of the
-            // first operand <-> lanes 0..31 of the second), lane (sub, h) holds columns 16h..16h+15 of row sub of
-            // the block: 16-byte chunk 4ib + 2h of the wave's 128-byte output row in w4[0], w4[2] and chunk
-            // 4ib + 2h + 1 in w4[1], w4[3].
+              for (int jb = 0; jb < 4; ++jb) {
+                const int mrow = min(m0 + wm * 128 + jb * 32 + esub, a.M - 1);
+                const v8bf uf =
+                    (k < a.r) ? *reinterpret_cast<const v8bf*>(a.u + (int64_t)mrow * a.ldu + k) : (v8bf){0};
+                c[i2][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[i2][jb], 0, 0, 0);
+              }
+            }
+          }
+          // Bias and bf16. After one exchange between the lane halves (v_permlane32_swap: lanes 32..63 of the
+          // first operand <-> lanes 0..31 of the second), lane (sub, h) holds columns 16h..16h+15 of row sub of
+          // the block: chunk 4ib + 2h in w4[0], w4[2] and chunk 4ib + 2h + 1 in w4[1], w4[3].
+          if (has_bias) {
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+              for (int v = 0; v < 16; ++v)
+                c[i2][jb][v] = c[i2][jb][v] + params[512 + wn * WN + ib * 32 + 8 * (v >> 2) + 4 * ehalf + (v & 3)];
+          }
+#pragma unroll
+          for (int jb = 0; jb < 4; ++jb) {
             uint32_t w4[4][2];
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
-              float v[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                v[e] = c[ib][jb][4 * gq + e];
-                v[e] = v[e] + params[512 + wn * 64 + ib * 32 + 8 * gq + 4 * ehalf + e];
-              }
-              w4[gq][0] = pack_bf16x2(v[0], v[1]);
-              w4[gq][1] = pack_bf16x2(v[2], v[3]);
+              w4[gq][0] = pack_bf16x2(c[i2][jb][4 * gq], c[i2][jb][4 * gq + 1]);
+              w4[gq][1] = pack_bf16x2(c[i2][jb][4 * gq + 2], c[i2][jb][4 * gq + 3]);
             }
 #pragma unroll
             for (int w = 0; w < 2; ++w) {
@@ -479,37 +487,73 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
               w4[1][w] = s13[0];
               w4[3][w] = s13[1];
             }
-            const int c0 = 4 * ib + 2 * ehalf;
-            *(v4i HF_LDS*)(stage_out + row * GBK + ((c0 ^ row_swz(row)) << 4)) =
-                (v4i){(int)w4[0][0], (int)w4[0][1], (int)w4[2][0], (int)w4[2][1]};
-            *(v4i HF_LDS*)(stage_out + row * GBK + (((c0 + 1) ^ row_swz(row)) << 4)) =
-                (v4i){(int)w4[1][0], (int)w4[1][1], (int)w4[3][0], (int)w4[3][1]};
+            pk[ib][jb][0] = w4[0][0];
+            pk[ib][jb][1] = w4[0][1];
+            pk[ib][jb][2] = w4[2][0];
+            pk[ib][jb][3] = w4[2][1];
+            pk[ib][jb][4] = w4[1][0];
+            pk[ib][jb][5] = w4[1][1];
+            pk[ib][jb][6] = w4[3][0];
+            pk[ib][jb][7] = w4[3][1];
           }
         }
-        wave_lds_sync();
+      }
+      // Every wave is done with the low-rank operands: the epilogue slot stages the output, 8 KiB per wave (64 rows
+      // of 128 bytes, swizzled like the operands), one round per pair of column blocks and half of the rows. Each
+      // lane then reads back 16 bytes of each of 8 rows, and each store instruction writes 8 whole 128-byte lines.
+      if constexpr (kLr) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        HF_BARRIER();
+      }
+      unsigned char HF_LDS* stage_out = eslot + wave * 8192;
+      uint16_t* out = static_cast<uint16_t*>(a.out);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int row = 8 * i + (el >> 3), ch = el & 7;
-          const v4i val = *(const v4i HF_LDS*)(stage_out + row * GBK + ((ch ^ row_swz(row)) << 4));
-          const int m = m0 + wm * 128 + 64 * rd + row;
-          const int n = n0 + wn * 64 + 8 * ch;
-          uint16_t* dst = out + (int64_t)m * a.ldo + n;
-          if (full) {
-            *reinterpret_cast<v4i*>(dst) = val;
-          } else if (m < a.M) {
-            if (a.out_vec16 && n + 8 <= a.N) {
-              *reinterpret_cast<v4i*>(dst) = val;
-            } else {
-              for (int e = 0; e < 8; ++e)
-                if (n + e < a.N) dst[e] = (uint16_t)((uint32_t)val[e >> 1] >> (16 * (e & 1)));
+      for (int pb = 0; pb < NB; pb += 2) {
+#pragma unroll
+        for (int rd = 0; rd < 2; ++rd) {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const int jb = 2 * rd + jj;
+            const int row = jj * 32 + esub;
+#pragma unroll
+            for (int i2 = 0; i2 < 2; ++i2) {
+              const int ib = pb + i2;
+              const int c0 = 4 * i2 + 2 * ehalf;
+              *(v4i HF_LDS*)(stage_out + row * GBK + ((c0 ^ row_swz(row)) << 4)) =
+                  (v4i){(int)pk[ib][jb][0], (int)pk[ib][jb][1], (int)pk[ib][jb][2], (int)pk[ib][jb][3]};
+              *(v4i HF_LDS*)(stage_out + row * GBK + (((c0 + 1) ^ row_swz(row)) << 4)) =
+                  (v4i){(int)pk[ib][jb][4], (int)pk[ib][jb][5], (int)pk[ib][jb][6], (int)pk[ib][jb][7]};
             }
           }
+          wave_lds_sync();
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int row = 8 * i + (el >> 3), ch = el & 7;
+            const v4i val = *(const v4i HF_LDS*)(stage_out + row * GBK + ((ch ^ row_swz(row)) << 4));
+            const int m = m0 + wm * 128 + 64 * rd + row;
+            const int n = n0 + wn * WN + 32 * pb + 8 * ch;
+            uint16_t* dst = out + (int64_t)m * a.ldo + n;
+            if (full) {
+              *reinterpret_cast<v4i*>(dst) = val;
+            } else if (m < a.M) {
+              if (a.out_vec16 && n + 8 <= a.N) {
+                *reinterpret_cast<v4i*>(dst) = val;
+              } else {
+                for (int e = 0; e < 8; ++e)
+                  if (n + e < a.N) dst[e] = (uint16_t)((uint32_t)val[e >> 1] >> (16 * (e & 1)));
+              }
+            }
+          }
+          wave_lds_sync();  // the next round rewrites this wave's staging area
         }
-        wave_lds_sync();  // the next round rewrites this wave's staging area
       }
     }
-    // A partial tile's guarded stores (and the r > 64 global reads) are not a fixed count: drain everything.
-    if (!full) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // A partial tile's guarded stores (and the r > 64 global reads) are not a fixed count, and too many stores do
+    // not fit the wait counter next to the next tile's loads: drain everything.
+    if (!full || kFastStores == 0) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      full = false;
+    }
     // Every wave is done with the epilogue slot: it receives the next tile's stage 1.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     HF_BARRIER();
