@@ -11,7 +11,15 @@ value = 2*M*N*K int8 ops per step / measured step time (TOPS). The roofline obje
 the timed region. The CPU baseline times the PyTorch-CPU path of the reference layer on a bounded row sample of the
 same workload on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+`--config N` runs one of the other measured workloads instead and prints one JSON line per shape (these are
+parity-test shapes and supporting measurements, not the headline line):
+  1  M=1024 K=3072 N=3072, rank 32, bias, 1% outlier channels x20
+  3  FFN pair on M=32768: up 5120->13824, tanh-GELU in bf16, down 13824->5120, rank 64
+  4  one DiT block's linears on M=41344: QKV 5120->15360, out 5120->5120, up 5120->13824, down 13824->5120, rank 64
+  5  small M in {64, 256, 1024}, K=5120, N in {5120, 30720}, rank 32: HBM GB/s over the compulsory bytes, with
+     enough weight copies rotated per step that the weights come from HBM, not the 256 MiB Infinity Cache
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--config N]
 """
 
 from __future__ import annotations
@@ -41,6 +49,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=32768, help="row sample for the CPU baseline")
+    p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
+                   help="workload: 2 (default) is the headline QKV projection; 1, 3, 4, 5 are supporting measurements")
     p.add_argument("--copy-probe", action="store_true",
                    help="only copy a 1 GiB device buffer 3 times (calibrates the HBM byte counters) and exit")
     return p.parse_args()
@@ -122,6 +132,10 @@ def main():
 
     if args.copy_probe:
         copy_probe(torch)
+        return
+    if args.config != 2:
+        for line in run_config(torch, args.config, args.steps, args.warmup):
+            print(json.dumps(line), flush=True)
         return
 
     from hyperflow_h3_flash_amd import Int8RotLinear
@@ -213,6 +227,119 @@ def main():
         torch.cuda.empty_cache()
         result["cpu_baseline"] = cpu_baseline(torch, args.cpu_rows)
     print(json.dumps(result), flush=True)
+
+
+# ------------------------------------------------------------------------------------------ supporting workloads
+
+
+def layer_inputs(torch, dev, m, k, n, rank, bias, outlier_frac, outlier_scale, seed, copies=1):
+    """Seeded synthetic inputs in the draw order x, outlier channels, qweight, wscale, down, up, bias; `copies`
+    independent weight sets for the same x (so a step can rotate through more weight bytes than the cache holds)."""
+    from hyperflow_h3_flash_amd import Int8RotLinear
+
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(m, k, device=dev, generator=gen)
+    cols = torch.randperm(k, device=dev, generator=gen)[: -(-k * int(outlier_frac * 1000) // 1000)]
+    x[:, cols] *= outlier_scale
+    x = x.to(torch.bfloat16)
+    layers = []
+    for _ in range(copies):
+        layer = Int8RotLinear(k, n, GROUP, rank=rank, bias=bias).to(dev)
+        with torch.no_grad():
+            layer.qweight.copy_(torch.randint(-127, 128, (n, k), device=dev, dtype=torch.int8, generator=gen))
+            layer.wscale.copy_(torch.rand(n, device=dev, generator=gen) * 9e-3 + 1e-3)
+            if rank:
+                layer.down.weight.copy_(torch.randn(rank, k, device=dev, generator=gen) * 0.02)
+                layer.up.weight.copy_(torch.randn(n, rank, device=dev, generator=gen) * 0.02)
+            if bias:
+                layer.bias.copy_(torch.randn(n, device=dev, generator=gen) * 0.01)
+        layers.append(layer)
+    return x, layers
+
+
+def timed(torch, fn, steps, warmup):
+    """Mean wall time per call in seconds, with the device synchronized around the timed calls."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def linear_bytes(m, k, n, rank, bias):
+    """Compulsory HBM bytes of one fused linear: x, qweight, wscale, low-rank down and up, bias, output."""
+    return 2 * m * k + n * k + 4 * n + 2 * rank * (k + n) + (2 * n if bias else 0) + 2 * m * n
+
+
+def run_config(torch, config, steps, warmup):
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    base = {"n_gpus": 1, "steps": steps, "warmup": warmup, "dtype": "int8", "data": "synthetic (seeded)",
+            "vs_baseline": None}
+    if config == 1:
+        m, k, n, r = 1024, 3072, 3072, 32
+        x, (layer,) = layer_inputs(torch, dev, m, k, n, r, True, 0.01, 20.0, seed=1)
+        with torch.no_grad():
+            t = timed(torch, lambda: layer(x), steps, warmup)
+        yield dict(base, metric="convrot INT8 linear TOPS, M=1024 K=3072 N=3072", unit="TOPS",
+                   value=round(2.0 * m * n * k / t / 1e12, 2), ms_per_step=round(t * 1e3, 4), higher_is_better=True,
+                   hbm_GBs=round(linear_bytes(m, k, n, r, True) / t / 1e9, 1),
+                   config={"workload": "single convrot linear", "M": m, "K": k, "N": n, "group": GROUP,
+                           "rank": r, "bias": True})
+    elif config in (3, 4):
+        if config == 3:
+            m, shapes, name = 32768, [(5120, 13824), (13824, 5120)], "FFN up + tanh-GELU + down"
+        else:
+            m = 41344
+            shapes, name = [(5120, 15360), (5120, 5120), (5120, 13824), (13824, 5120)], "DiT block linears"
+        built = [layer_inputs(torch, dev, m, k, n, 64, False, 0.005, 30.0, seed=3 + i) for i, (k, n) in
+                 enumerate(shapes)]
+        xs = [b[0] for b in built]
+        layers = [b[1][0] for b in built]
+
+        def step():
+            with torch.no_grad():
+                if config == 3:
+                    h = layers[0](xs[0])
+                    h = torch.nn.functional.gelu(h, approximate="tanh")
+                    layers[1](h)
+                else:
+                    for x, layer in zip(xs, layers):
+                        layer(x)
+
+        t = timed(torch, step, steps, warmup)
+        ops = sum(2.0 * m * n * k for k, n in shapes)
+        yield dict(base, metric=f"convrot INT8 {name} TOPS, M={m}", unit="TOPS", value=round(ops / t / 1e12, 2),
+                   ms_per_step=round(t * 1e3, 4), higher_is_better=True,
+                   pct_of_peak=round(100.0 * ops / t / 1e12 / PEAK_INT8_TOPS, 2),
+                   config={"workload": name, "M": m, "shapes_KN": shapes, "group": GROUP, "rank": 64,
+                           "bias": False})
+    else:
+        k = 5120
+        for m in (64, 256, 1024):
+            for n in (5120, 30720):
+                copies = max(1, -(-(600 << 20) // (n * k)))  # > 600 MB of weights per pass through the copies
+                x, layers = layer_inputs(torch, dev, m, k, n, 32, False, 0.005, 30.0, seed=5, copies=copies)
+                state = {"i": 0}
+
+                def step():
+                    with torch.no_grad():
+                        layers[state["i"] % copies](x)
+                    state["i"] += 1
+
+                t = timed(torch, step, steps * copies, warmup)
+                nbytes = linear_bytes(m, k, n, 32, False)
+                yield dict(base, metric=f"convrot INT8 linear HBM GB/s, M={m} K={k} N={n}", unit="GB/s",
+                           value=round(nbytes / t / 1e9, 1), ms_per_step=round(t * 1e3, 4), higher_is_better=True,
+                           pct_of_hbm_peak=round(100.0 * nbytes / t / 1e9 / PEAK_HBM_GBS, 2),
+                           tops=round(2.0 * m * n * k / t / 1e12, 2),
+                           config={"workload": "small-M convrot linear", "M": m, "K": k, "N": n, "group": GROUP,
+                                   "rank": 32, "bias": False, "weight_copies": copies})
+                del x, layers
+                torch.cuda.empty_cache()
 
 
 if __name__ == "__main__":

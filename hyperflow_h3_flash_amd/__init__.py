@@ -13,6 +13,7 @@ from .int8 import (
     resolve_int8_gemm,
     set_kernel_options,
 )
+from .lowrank import RANK_MULTIPLE, LowRankLinear, fuse_qkv, set_lowrank_rank_multiple
 
 __version__ = "0.1.0"
 
@@ -21,8 +22,12 @@ __all__ = [
     "KERNEL_OPTIONS",
     "ROTATE_QUANTS",
     "Int8RotLinear",
+    "LowRankLinear",
+    "RANK_MULTIPLE",
+    "fuse_qkv",
     "hadamard_factors",
     "regular_hadamard",
     "resolve_int8_gemm",
     "set_kernel_options",
+    "set_lowrank_rank_multiple",
 ]

@@ -8,16 +8,25 @@
 * `quantize_weight` — the checkpoint format ``qweight = round(W R / wscale)``, ``wscale = absmax_row(W R) / 127``,
   computed in float64 (tests/test_int8.py:31-36). An offline conversion step for bf16/fp32 weights, not part of the
   forward pass.
+* `prepare_model` / `load_partition` / `save_partition` — a checkpoint partition such as ``fl2va_int8_convrot``: a
+  folder with ``config.json`` (its ``lowrank_ranks`` and ``quantization`` blocks build the layers,
+  transformer.py:185-203) and safetensors shards (an optional ``*.safetensors.index.json`` lists them). Tensors are
+  read with the safetensors loader, which executes nothing from the file. ``qweight`` stays int8 and ``wscale``
+  stays fp32 whatever the model's dtype, as the reference's ``_keep_in_fp32_modules`` keeps them
+  (transformer.py:129-133, tests/test_transformer.py:164-175); other floating tensors take the model's dtype.
 """
 
 from __future__ import annotations
 
+import json
+import os
 from typing import Any
 
 import torch
 from torch import Tensor, nn
 
 from .int8 import Int8RotLinear, regular_hadamard
+from .lowrank import LowRankLinear
 
 METHOD = "int8_convrot"
 
@@ -29,7 +38,9 @@ def replace_linear(model: nn.Module, name: str, make: type[nn.Module], *args: An
     dense = owner[int(attr)] if isinstance(owner, nn.ModuleList) else getattr(owner, attr)
     if type(dense) is not nn.Linear or dense.bias is not None:
         raise TypeError(f"{name} is not a bias-free nn.Linear")
-    replacement = make(dense.in_features, dense.out_features, *args, **kwargs)
+    replacement = make(dense.in_features, dense.out_features, *args, **kwargs).to(dense.weight.device)
+    if isinstance(replacement, LowRankLinear):
+        replacement.to(dense.weight.dtype)  # the factors take the model's dtype; INT8 storage dtypes are fixed
     if isinstance(owner, nn.ModuleList):
         owner[int(attr)] = replacement
     else:
@@ -78,4 +89,113 @@ def load_quantized(layer: Int8RotLinear, weight: Tensor) -> Int8RotLinear:
     return layer
 
 
-__all__ = ["METHOD", "apply_quantization", "load_quantized", "quantize_weight", "replace_linear"]
+CONFIG_NAME = "config.json"
+#: Leaves stored in their own dtype whatever the model's (int8 codes, fp32 per-channel scales).
+STORAGE_DTYPE_LEAVES = ("qweight", "wscale")
+
+
+def read_config(folder: str) -> dict[str, Any]:
+    with open(os.path.join(folder, CONFIG_NAME)) as f:
+        return json.load(f)
+
+
+def prepare_model(model: nn.Module, config: dict[str, Any]) -> nn.Module:
+    """Build the compressed layers a partition's ``config.json`` names: `LowRankLinear` for every entry of
+    ``lowrank_ranks`` and `Int8RotLinear` for the ``quantization`` block (transformer.py:185-203)."""
+    for name, rank in (config.get("lowrank_ranks") or {}).items():
+        replace_linear(model, name, LowRankLinear, int(rank))
+    apply_quantization(model, config.get("quantization"))
+    return model
+
+
+def shard_files(folder: str) -> list[str]:
+    """The partition's safetensors shards: those its index lists (all must exist), else every ``*.safetensors``."""
+    indexes = sorted(f for f in os.listdir(folder) if f.endswith(".safetensors.index.json"))
+    if indexes:
+        files: list[str] = []
+        for index in indexes:
+            with open(os.path.join(folder, index)) as f:
+                files += sorted(set(json.load(f)["weight_map"].values()))
+        missing = [f for f in files if not os.path.isfile(os.path.join(folder, f))]
+        if missing:
+            raise FileNotFoundError(f"{folder}: shards listed in the index are missing: {missing}")
+        return [os.path.join(folder, f) for f in files]
+    files = sorted(f for f in os.listdir(folder) if f.endswith(".safetensors"))
+    if not files:
+        raise FileNotFoundError(f"{folder}: no safetensors shards")
+    return [os.path.join(folder, f) for f in files]
+
+
+@torch.no_grad()
+def load_partition(model: nn.Module, folder: str, *, prepare: bool = True, strict: bool = True,
+                   dtype: torch.dtype | None = None) -> tuple[list[str], list[str]]:
+    """Load a checkpoint partition into ``model`` (built by `prepare_model` from its ``config.json`` first unless
+    ``prepare=False``). Returns ``(missing, unexpected)`` keys; with ``strict`` either being non-empty raises.
+
+    Every tensor lands on the device of the parameter or buffer it replaces. ``qweight`` and ``wscale`` keep their
+    storage dtypes; other floating tensors are cast to ``dtype`` (default: the replaced tensor's dtype)."""
+    from safetensors.torch import load_file
+
+    if prepare:
+        prepare_model(model, read_config(folder))
+    targets = dict(model.named_parameters())
+    targets.update(dict(model.named_buffers()))
+    seen: set[str] = set()
+    unexpected: list[str] = []
+    for path in shard_files(folder):
+        for key, tensor in load_file(path, device="cpu").items():
+            if key not in targets:
+                unexpected.append(key)
+                continue
+            current = targets[key]
+            if tuple(current.shape) != tuple(tensor.shape):
+                raise ValueError(f"{key}: checkpoint shape {tuple(tensor.shape)} != model {tuple(current.shape)}")
+            leaf = key.rpartition(".")[2]
+            if leaf in STORAGE_DTYPE_LEAVES or not tensor.is_floating_point():
+                target_dtype = tensor.dtype
+            else:
+                target_dtype = dtype or current.dtype
+            value = tensor.to(device=current.device, dtype=target_dtype)
+            owner_name, _, attr = key.rpartition(".")
+            owner = model.get_submodule(owner_name) if owner_name else model
+            if attr in owner._parameters:
+                owner._parameters[attr] = nn.Parameter(value, requires_grad=current.requires_grad)
+            else:
+                owner._buffers[attr] = value
+            seen.add(key)
+    missing = sorted(set(targets) - seen)
+    if strict and (missing or unexpected):
+        raise RuntimeError(f"checkpoint does not match the model: missing {missing}, unexpected {unexpected}")
+    return missing, unexpected
+
+
+def save_partition(model: nn.Module, folder: str, config: dict[str, Any], *, max_shard_bytes: int = 5 << 30) -> list[str]:
+    """Write ``config.json`` and the model's state dict as safetensors shards (with an index when there is more than
+    one); returns the shard paths."""
+    from safetensors.torch import save_file
+
+    os.makedirs(folder, exist_ok=True)
+    with open(os.path.join(folder, CONFIG_NAME), "w") as f:
+        json.dump(config, f, indent=2, sort_keys=True)
+    shards: list[dict[str, Tensor]] = [{}]
+    size = 0
+    for key, tensor in model.state_dict().items():
+        nbytes = tensor.numel() * tensor.element_size()
+        if shards[-1] and size + nbytes > max_shard_bytes:
+            shards.append({})
+            size = 0
+        shards[-1][key] = tensor.detach().to("cpu").contiguous()
+        size += nbytes
+    names = (["diffusion_pytorch_model.safetensors"] if len(shards) == 1 else
+             [f"diffusion_pytorch_model-{i + 1:05d}-of-{len(shards):05d}.safetensors" for i in range(len(shards))])
+    for name, shard in zip(names, shards):
+        save_file(shard, os.path.join(folder, name))
+    if len(shards) > 1:
+        weight_map = {key: name for name, shard in zip(names, shards) for key in shard}
+        with open(os.path.join(folder, "diffusion_pytorch_model.safetensors.index.json"), "w") as f:
+            json.dump({"metadata": {}, "weight_map": weight_map}, f, indent=2, sort_keys=True)
+    return [os.path.join(folder, n) for n in names]
+
+
+__all__ = ["CONFIG_NAME", "METHOD", "apply_quantization", "load_partition", "load_quantized", "prepare_model",
+           "quantize_weight", "read_config", "replace_linear", "save_partition", "shard_files"]

@@ -47,6 +47,8 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLrLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<2>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLrLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_up_kernel),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kUpLds);
     (void)hipGetLastError();
   });
 }
@@ -163,6 +165,25 @@ int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_
     if (st != HF_OK) return st;
   }
   return HF_OK;
+}
+
+int hf_lowrank_up(const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
+                  uint16_t* y, int64_t ldy, int64_t M, int64_t N, hf_stream_t stream) {
+  if (M < 0 || N < 0 || r < 0 || ldu < r || ld_up < r || ldy < N) return HF_ERR_ARGUMENT;
+  if (M == 0 || N == 0) return HF_OK;
+  if (!y || (r > 0 && (!u || !up))) return HF_ERR_ARGUMENT;
+  if ((r % 8) || (r > 0 && (!aligned(u, 16) || !aligned(up, 16))) || (ldu % 8) || (ld_up % 8) || !aligned(y, 2))
+    return HF_ERR_ALIGNMENT;
+  if (M >= (int64_t(1) << 31) || N >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  if (2 * hf::kUpTile * std::max(ldu, ld_up) >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  allow_large_lds();
+  const int64_t tiles_n = (N + hf::kUpTile - 1) / hf::kUpTile, tiles = ((M + hf::kUpTile - 1) / hf::kUpTile) * tiles_n;
+  if (tiles >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  const int vec16 = aligned(y, 16) && (ldy % 8) == 0;
+  hipLaunchKernelGGL(hf::lowrank_up_kernel, dim3((unsigned)tiles), dim3(hf::kUpThreads), hf::kUpLds,
+                     static_cast<hipStream_t>(stream), u, ldu, up, ld_up, bias, y, ldy, (int)M, (int)N, (int)r,
+                     (int)tiles_n, vec16);
+  return launch_status();
 }
 
 int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,

@@ -37,7 +37,7 @@ __device__ __forceinline__ void lr_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t oo
     const int row = blk * 8 + (lane >> 3);
     const int c = lr_swizzle(row, lane & 7);
     const int k = k0 + c * 8;
-    const uint32_t voff = (row < rows_valid && k < K) ? (uint32_t)row * ld_bytes + (uint32_t)k * 2u : oob;
+    const uint32_t voff = ((row < rows_valid) & (k < K)) ? (uint32_t)row * ld_bytes + (uint32_t)k * 2u : oob;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + blk * 1024), 16, voff, 0, 0, 0);
   }
 }
@@ -120,5 +120,144 @@ template __global__ void lowrank_down_kernel<1>(const uint16_t*, int64_t, const 
                                                 int64_t, int, int, int);
 template __global__ void lowrank_down_kernel<2>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
                                                 int64_t, int, int, int);
+
+// Low-rank up projection y = bf16(u @ up^T + bias), the second half of LowRankLinear.forward
+// (src/hyperflow_h3_flash/transformer.py:57-58: `self.up(...)`, a bias-free bf16 nn.Linear; the bias is this build's
+// extension). u is [M, r] bf16 (the output of lowrank_down_kernel), up is [N, r] bf16 (nn.Linear weight layout).
+//
+// One workgroup per 128 x 128 output tile, 4 waves of 64 x 64 (2 x 2 blocks of v_mfma_f32_32x32x16_bf16, first
+// operand up, second u: lanes end with four consecutive n of one row m). The rank is consumed in chunks of 64: the
+// chunk's u rows and up rows (128 bytes each, swizzled with swizzle128) go global -> LDS with buffer_load ... lds,
+// 8 lanes per row. The output is the dominant traffic (2 bytes per element); it leaves through LDS so every store
+// instruction writes 8 whole 128-byte lines.
+constexpr int kUpTile = 128;
+constexpr int kUpThreads = 256;
+constexpr int kUpLds = 2 * kUpTile * 128 + kUpTile * 4;  // u and up chunks (16 KiB each) + the tile's bias (fp32)
+
+__global__ __launch_bounds__(kUpThreads) void lowrank_up_kernel(const uint16_t* __restrict__ u, int64_t ldu,
+                                                                 const uint16_t* __restrict__ up, int64_t ldup,
+                                                                 const uint16_t* __restrict__ bias,
+                                                                 uint16_t* __restrict__ y, int64_t ldy, int M, int N,
+                                                                 int r, int tiles_n, int out_vec16) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char up_smem_raw[];
+  unsigned char HF_LDS* smem = (unsigned char HF_LDS*)up_smem_raw;
+  unsigned char HF_LDS* u_lds = smem;
+  unsigned char HF_LDS* up_lds = smem + kUpTile * 128;
+  float HF_LDS* bias_lds = (float HF_LDS*)(smem + 2 * kUpTile * 128);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int sub = lane & 31, half = lane >> 5;
+  const int m0 = (blockIdx.x / tiles_n) * kUpTile, n0 = (blockIdx.x % tiles_n) * kUpTile;
+  const int rows_m = min(kUpTile, M - m0), rows_n = min(kUpTile, N - n0);
+
+  if (threadIdx.x < kUpTile) {
+    const int n = n0 + threadIdx.x;
+    bias_lds[threadIdx.x] = (bias && n < N) ? __uint_as_float((uint32_t)bias[n] << 16) : 0.0f;
+  }
+  __syncthreads();  // the bias is read in the epilogue (a rank of zero runs no chunk barrier)
+  const uint32_t ldu_bytes = (uint32_t)ldu * 2u, ldup_bytes = (uint32_t)ldup * 2u;
+  const uint32_t bytes_u = (uint32_t)rows_m * ldu_bytes, bytes_up = (uint32_t)rows_n * ldup_bytes;
+  const __amdgpu_buffer_rsrc_t ru = make_rsrc(u + (int64_t)m0 * ldu, bytes_u);
+  const __amdgpu_buffer_rsrc_t rup = make_rsrc(up + (int64_t)n0 * ldup, bytes_up);
+
+  v16f acc[2][2];
+#pragma unroll
+  for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) acc[ib][jb] = (v16f){0};
+
+  for (int c0 = 0; c0 < r; c0 += 64) {
+    // 16 blocks of 8 rows per operand, 4 per wave; chunks past r and rows past the tile read as zero.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool isup = i >= 4;
+      const int blk = 4 * wave + (i & 3), row = 8 * blk + (lane >> 3);
+      const int c = (lane & 7) ^ (((lane >> 3) ^ blk) & 7);
+      const int rows_valid = isup ? rows_n : rows_m;
+      const uint32_t ldb = isup ? ldup_bytes : ldu_bytes, oob = isup ? bytes_up : bytes_u;
+      const uint32_t voff = ((row < rows_valid) & (c0 + 8 * c < r)) ? row * ldb + (uint32_t)(c0 + 8 * c) * 2u : oob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(isup ? rup : ru, (void HF_LDS*)((isup ? up_lds : u_lds) + blk * 1024),
+                                               16, voff, 0, 0, 0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int kk = 0; kk < 64; kk += 16) {
+      const int chunk = kk / 8 + half;
+      v8bf pf[2], uf[2];
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        const int nl = wn * 64 + ib * 32 + sub;
+        pf[ib] = *(const v8bf HF_LDS*)(up_lds + nl * 128 + (swizzle128(nl, chunk) << 4));
+      }
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        const int ml = wm * 64 + jb * 32 + sub;
+        uf[jb] = *(const v8bf HF_LDS*)(u_lds + ml * 128 + (swizzle128(ml, chunk) << 4));
+      }
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb)
+          acc[ib][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf[ib], uf[jb], acc[ib][jb], 0, 0, 0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // the next chunk (or the staging) rewrites LDS
+  }
+
+  // Bias, bf16, and the output through LDS: lane (sub, h) holds columns 16h..16h+15 of row sub of each block after
+  // one exchange between the lane halves; the wave stages its 64 x 64 tile (64 rows of 128 bytes) and stores 8 whole
+  // rows per instruction.
+  unsigned char HF_LDS* stage_out = smem + wave * 8192;
+#pragma unroll
+  for (int jb = 0; jb < 2; ++jb) {
+    const int row = jb * 32 + sub;
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+      uint32_t w4[4][2];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = acc[ib][jb][4 * gq + e] + bias_lds[wn * 64 + ib * 32 + 8 * gq + 4 * half + e];
+        w4[gq][0] = pack_bf16x2(v[0], v[1]);
+        w4[gq][1] = pack_bf16x2(v[2], v[3]);
+      }
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        const auto s02 = __builtin_amdgcn_permlane32_swap(w4[0][w], w4[2][w], false, false);
+        const auto s13 = __builtin_amdgcn_permlane32_swap(w4[1][w], w4[3][w], false, false);
+        w4[0][w] = s02[0];
+        w4[2][w] = s02[1];
+        w4[1][w] = s13[0];
+        w4[3][w] = s13[1];
+      }
+      const int c0 = 4 * ib + 2 * half;
+      *(v4i HF_LDS*)(stage_out + row * 128 + (swizzle128(row, c0) << 4)) =
+          (v4i){(int)w4[0][0], (int)w4[0][1], (int)w4[2][0], (int)w4[2][1]};
+      *(v4i HF_LDS*)(stage_out + row * 128 + (swizzle128(row, c0 + 1) << 4)) =
+          (v4i){(int)w4[1][0], (int)w4[1][1], (int)w4[3][0], (int)w4[3][1]};
+    }
+  }
+  wave_lds_sync();
+  const bool full = rows_m == kUpTile && rows_n == kUpTile && out_vec16;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 8 * i + (lane >> 3), ch = lane & 7;
+    const v4i val = *(const v4i HF_LDS*)(stage_out + row * 128 + (swizzle128(row, ch) << 4));
+    const int m = m0 + wm * 64 + row, n = n0 + wn * 64 + 8 * ch;
+    uint16_t* dst = y + (int64_t)m * ldy + n;
+    if (full) {
+      *reinterpret_cast<v4i*>(dst) = val;
+    } else if (m < M) {
+      if (out_vec16 && n + 8 <= N) {
+        *reinterpret_cast<v4i*>(dst) = val;
+      } else {
+        for (int e = 0; e < 8; ++e)
+          if (n + e < N) dst[e] = (uint16_t)((uint32_t)val[e >> 1] >> (16 * (e & 1)));
+      }
+    }
+  }
+}
 
 }  // namespace hf

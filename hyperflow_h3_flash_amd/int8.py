@@ -224,6 +224,24 @@ def lowrank_down(x: Tensor, down: Tensor) -> Tensor:
     return u
 
 
+def lowrank_up(u: Tensor, up: Tensor, bias: Tensor | None = None) -> Tensor:
+    """``bf16(u @ up^T [+ bias])`` for u bf16 [M, r] and up bf16 [N, r] (LowRankLinear.up, transformer.py:57-58)."""
+    M, r = u.shape
+    N = up.shape[0]
+    if up.shape[1] != r:
+        raise ValueError(f"rank mismatch: {tuple(u.shape)} vs {tuple(up.shape)}")
+    _same_device(u.device, up, bias)
+    u, up = _pad_rank(u.to(torch.bfloat16), up.to(torch.bfloat16))
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    y = torch.empty(M, N, device=u.device, dtype=torch.bfloat16)
+    with torch.cuda.device(u.device):
+        status = _native.library().hf_lowrank_up(_ptr(u), u.stride(0), _ptr(up), up.stride(0), u.shape[1],
+                                                 _ptr(bias), _ptr(y), y.stride(0), M, N, _stream(u.device))
+    _check(status, "hf_lowrank_up")
+    return y
+
+
 def _pad_rank(u: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
     # The kernel reads the rank in 8-wide chunks; zero columns add exact zeros (transformer.py:60-73).
     r = u.shape[1]
@@ -285,6 +303,7 @@ def _kernels() -> SimpleNamespace:
         rotate_quant=rotate_quant,
         int8_matmul=int8_matmul,
         lowrank_down=lowrank_down,
+        lowrank_up=lowrank_up,
         int8_gemm_i32=int8_gemm_i32,
         backend=BACKEND,
     )

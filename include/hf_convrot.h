@@ -14,6 +14,7 @@
  *   hf_int8_linear    <- `_kernels().int8_matmul(a, b, sa, sb)`            int8.py:376-390 (kernel int8.py:283-313)
  *                        extended with the low-rank + bias epilogue of      transformer.py:57-58
  *   hf_lowrank_down   <- `LowRankLinear.down(x)` (bf16 nn.Linear)          transformer.py:57-58
+ *   hf_lowrank_up     <- `LowRankLinear.up(u)` (bf16 nn.Linear)            transformer.py:57-58
  *   hf_int8_gemm_i32  <- the int32 accumulator of `int8_mm_kernel`         int8.py:302-306 (torch._int_mm, :362)
  *   hf_convrot_linear <- `Int8RotLinear.forward` device branch             int8.py:161-171
  */
@@ -60,6 +61,17 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
  */
 int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_t ld_down, uint16_t* u,
                     int64_t ldu, int64_t M, int64_t K, int32_t r, hf_stream_t stream);
+
+/*
+ * Low-rank up projection y = bf16(u @ up^T [+ bias]) (LowRankLinear.up, a bias-free bf16 nn.Linear,
+ * transformer.py:57-58; the bias is an extension, NULL for none). Together with hf_lowrank_down this is the whole
+ * LowRankLinear forward. fp32 accumulation over the rank, one rounding to bf16 (round to nearest even).
+ * u: bf16 [M, ldu]; up: bf16 [N, ld_up] (nn.Linear(r, N).weight); bias: bf16 [N] or NULL; y: bf16 [M, ldy].
+ * Requires: r % 8 == 0 (zero-pad the rank: an exact no-op); u and up 16-byte aligned; ldu % 8 == 0;
+ * ld_up % 8 == 0; y 2-byte aligned (16-byte aligned with ldy % 8 == 0 for whole-line stores).
+ */
+int hf_lowrank_up(const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
+                  uint16_t* y, int64_t ldy, int64_t M, int64_t N, hf_stream_t stream);
 
 /*
  * Fused INT8 linear:

@@ -196,6 +196,18 @@ def lowrank_down(x_bits: np.ndarray, down_bits: np.ndarray) -> np.ndarray:
     return u
 
 
+def lowrank_up(u_bits: np.ndarray, up_bits: np.ndarray, bias_bits: np.ndarray | None = None) -> np.ndarray:
+    """``bf16(u @ up^T [+ bias])``: LowRankLinear's second bf16 nn.Linear (transformer.py:57-58), the exact sum
+    (float64: products of bf16 values are exact and r <= 2^20 terms stay far inside 53 bits for these magnitudes)
+    rounded once. The bias is this build's extension."""
+    u = bf16_to_f32(np.asarray(u_bits, dtype=np.uint16)).astype(np.float64)
+    up = bf16_to_f32(np.asarray(up_bits, dtype=np.uint16)).astype(np.float64)
+    y = u @ up.T
+    if bias_bits is not None:
+        y = y + bf16_to_f32(np.asarray(bias_bits, dtype=np.uint16)).astype(np.float64)[None, :]
+    return f64_to_bf16(y)
+
+
 def fused_epilogue(acc, sx, wscale, u_bits=None, up_bits=None, bias_bits=None) -> np.ndarray:
     """The fused extension's definition: ``bf16((f32(acc)*sx)*ws + u @ up^T + bias)`` rounded once."""
     acc = np.ascontiguousarray(acc, dtype=np.int32)

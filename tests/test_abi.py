@@ -69,5 +69,9 @@ def test_argument_checks_reject_before_launching(lib):
     assert lib.hf_int8_gemm_i32(fake, 128, fake, 128, odd, 64, 4, 64, 128, null) == -3
     assert lib.hf_lowrank_down(fake, 128, fake, 128, fake, 4, 4, 128, 8, null) == -1  # ldu < r
     assert lib.hf_lowrank_down(fake, 128, fake, 128, fake, 8, 4, 120, 8, null) == -3  # K % 16
+    assert lib.hf_lowrank_up(fake, 8, fake, 8, 16, null, fake, 64, 4, 64, null) == -1  # ldu < r
+    assert lib.hf_lowrank_up(fake, 16, fake, 16, 12, null, fake, 64, 4, 64, null) == -3  # r % 8
+    assert lib.hf_lowrank_up(odd, 16, fake, 16, 16, null, fake, 64, 4, 64, null) == -3  # u alignment
+    assert lib.hf_lowrank_up(null, 16, null, 16, 16, null, null, 64, 0, 64, null) == 0  # no rows: no-op
     # sizes beyond the kernels' index range
     assert lib.hf_int8_gemm_i32(fake, 1 << 24, fake, 128, fake, 64, 4, 64, 128, null) == -5

@@ -111,3 +111,123 @@ def test_dequantized_weight_reconstructs_the_dense_one(oracle_lib):
     h = torch.block_diag(*[torch.from_numpy(oracle_lib.regular_hadamard(16))] * 8).double()
     back = (q.double() * ws.double()[:, None]) @ h.T
     assert ((back - w.double()).norm() / w.double().norm()) < 0.01
+
+
+# ------------------------------------------------------------------------------------------ checkpoint partitions
+
+RANKS = {"transformer_blocks.0.attn.to_q": 8, "transformer_blocks.0.attn.to_out.0": 16}
+
+
+def partition_config():
+    return {"lowrank_ranks": dict(RANKS), "quantization": dict(QUANT), "dropped_blocks": []}
+
+
+def filled_model(seed=0):
+    from hyperflow_h3_flash_amd.convert import load_quantized, prepare_model
+
+    torch.manual_seed(seed)
+    model = prepare_model(Toy(), partition_config())
+    for module in model.modules():
+        if isinstance(module, Int8RotLinear):
+            load_quantized(module, torch.randn(module.out_features, module.in_features) * 0.02)
+    return model
+
+
+def test_save_and_load_keep_the_storage_dtypes(tmp_path):
+    """tests/test_transformer.py:164-175: qweight int8 and wscale fp32 under a bf16 model; low-rank factors bf16."""
+    from hyperflow_h3_flash_amd import LowRankLinear
+    from hyperflow_h3_flash_amd.convert import load_partition, save_partition
+
+    model = filled_model()
+    save_partition(model, str(tmp_path), partition_config())
+    fresh = Toy().to(torch.bfloat16)
+    missing, unexpected = load_partition(fresh, str(tmp_path))
+    assert missing == [] and unexpected == []
+    assert isinstance(fresh.transformer_blocks[0].attn.to_q, LowRankLinear)
+    assert fresh.transformer_blocks[0].attn.to_q.rank == 8
+    layer = fresh.transformer_blocks[2].attn.to_k
+    assert layer.qweight.dtype == torch.int8 and layer.wscale.dtype == torch.float32
+    assert layer.keep_input is True
+    assert fresh.transformer_blocks[0].attn.to_q.down.weight.dtype == torch.bfloat16
+    assert fresh.proj.weight.dtype == torch.bfloat16
+    for key, value in model.state_dict().items():
+        got = fresh.state_dict()[key]
+        if value.dtype in (torch.int8, torch.float32) and key.endswith(("qweight", "wscale")):
+            assert torch.equal(got, value), key
+        else:
+            torch.testing.assert_close(got.float(), value.to(torch.bfloat16).float(), rtol=0, atol=0)
+
+
+def test_sharded_partition_with_an_index(tmp_path):
+    from hyperflow_h3_flash_amd.convert import load_partition, save_partition, shard_files
+
+    model = filled_model(1)
+    paths = save_partition(model, str(tmp_path), partition_config(), max_shard_bytes=8 << 10)
+    assert len(paths) > 2 and (tmp_path / "diffusion_pytorch_model.safetensors.index.json").exists()
+    assert shard_files(str(tmp_path)) == sorted(paths)
+    fresh = Toy()
+    load_partition(fresh, str(tmp_path))
+    for key, value in model.state_dict().items():
+        assert torch.equal(fresh.state_dict()[key], value), key
+    # a shard the index lists is missing: refuse rather than load a partial model
+    import os
+
+    os.remove(paths[1])
+    with pytest.raises(FileNotFoundError, match="missing"):
+        load_partition(Toy(), str(tmp_path))
+
+
+def test_partition_mismatches_are_reported(tmp_path):
+    from hyperflow_h3_flash_amd.convert import load_partition, save_partition
+
+    model = filled_model(2)
+    save_partition(model, str(tmp_path), partition_config())
+    # a model built without the quantization block has dense weights where the file has qweight/wscale
+    with pytest.raises(RuntimeError, match="does not match"):
+        load_partition(Toy(), str(tmp_path), prepare=False)
+    missing, unexpected = load_partition(Toy(), str(tmp_path), prepare=False, strict=False)
+    assert "transformer_blocks.2.attn.to_k.qweight" in unexpected
+    assert "transformer_blocks.2.attn.to_k.weight" in missing
+    bad = partition_config()
+    bad["quantization"]["method"] = "fp8"
+    save_partition(model, str(tmp_path / "bad"), bad)
+    with pytest.raises(ValueError, match="unsupported quantization method"):
+        load_partition(Toy(), str(tmp_path / "bad"))
+
+
+def test_rank_padding_keeps_the_factors():
+    """transformer.py:60-73 and 285-317: zero rows of down / columns of up; trimming restores the used rank."""
+    from hyperflow_h3_flash_amd import LowRankLinear, set_lowrank_rank_multiple
+
+    torch.manual_seed(0)
+    model = nn.Module()
+    model.a = LowRankLinear(64, 32, 8)
+    model.b = LowRankLinear(64, 48, 16)
+    model.b.down.weight.data[5:] = 0
+    model.b.up.weight.data[:, 5:] = 0
+    dense = {name: (m.up.weight @ m.down.weight).detach().clone() for name, m in (("a", model.a), ("b", model.b))}
+    assert model.a.pad_rank(64) and not model.a.pad_rank(64)
+    assert (model.a.rank, model.a.down.weight.shape, model.a.up.weight.shape) == (64, (64, 64), (32, 64))
+    assert set_lowrank_rank_multiple(model, 8) == 2
+    assert (model.a.rank, model.b.rank, model.b.down.out_features, model.b.up.in_features) == (8, 8, 8, 8)
+    assert set_lowrank_rank_multiple(model, 8) == 0
+    assert set_lowrank_rank_multiple(model, 0) == 1 and model.b.rank == 5
+    for name, m in (("a", model.a), ("b", model.b)):
+        torch.testing.assert_close(m.up.weight @ m.down.weight, dense[name], rtol=0, atol=0)
+
+
+def test_fuse_qkv_checks_its_inputs():
+    from hyperflow_h3_flash_amd import fuse_qkv
+
+    a, b = Int8RotLinear(64, 32, 16), Int8RotLinear(64, 48, 16)
+    fused = fuse_qkv(a, b)
+    assert (fused.in_features, fused.out_features, fused.group) == (64, 80, 16)
+    assert torch.equal(fused.qweight, torch.cat([a.qweight, b.qweight]))
+    with pytest.raises(ValueError, match="in_features"):
+        fuse_qkv(a, Int8RotLinear(128, 32, 16))
+    with pytest.raises(ValueError, match="group"):
+        fuse_qkv(a, Int8RotLinear(64, 32, 64))
+    with pytest.raises(ValueError, match="rank"):
+        fuse_qkv(a, Int8RotLinear(64, 32, 16, rank=8))
+    with pytest.raises(ValueError):
+        fuse_qkv()

@@ -1,0 +1,120 @@
+"""The standalone low-rank linear and the fused Q/K/V projection on the gfx950 kernels.
+
+Bars: the low-rank branch within one bf16 ulp of the oracle's exactly rounded sums (the device sums in fp32, the
+oracle in float64) and bitwise on almost every element; zero-padded ranks and the fused Q/K/V projection bitwise
+equal to the unpadded / separate layers.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    if not torch.cuda.is_available():
+        pytest.fail("no ROCm device visible")
+    from hyperflow_h3_flash_amd import _native
+
+    _native.library()
+
+
+def to_dev_bf16(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def bits_of(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def within_one_ulp(got_bits, ref_bits, lib):
+    got, ref = lib.bf16_to_f32(got_bits), lib.bf16_to_f32(ref_bits)
+    return (np.abs(got - ref) <= np.abs(ref) * 2.0**-7 + 1e-30).all(), (got == ref).mean()
+
+
+@pytest.mark.parametrize("m,n,r,bias", [(1, 8, 8, False), (100, 200, 64, True), (300, 520, 136, False),
+                                        (257, 1000, 200, True), (128, 128, 8, False)])
+def test_lowrank_up_matches_oracle(oracle_lib, m, n, r, bias):
+    from hyperflow_h3_flash_amd.int8 import lowrank_up
+
+    rng = np.random.default_rng(m + n + r)
+    u = oracle_lib.f32_to_bf16(rng.standard_normal((m, r)).astype(np.float32))
+    up = oracle_lib.f32_to_bf16((rng.standard_normal((n, r)) * 0.02).astype(np.float32))
+    b = oracle_lib.f32_to_bf16((rng.standard_normal(n) * 0.01).astype(np.float32)) if bias else None
+    y = lowrank_up(to_dev_bf16(u), to_dev_bf16(up), None if b is None else to_dev_bf16(b))
+    ok, exact = within_one_ulp(bits_of(y), oracle_lib.lowrank_up(u, up, b), oracle_lib)
+    assert ok and exact > 0.98
+
+
+def test_lowrank_linear_matches_the_reference_composition(oracle_lib):
+    """`LowRankLinear(x) = up(down(x))` against the reference modules' own output (the composition fixture)."""
+    from golden_utils import load_fixture
+
+    from hyperflow_h3_flash_amd import LowRankLinear
+
+    f = load_fixture("composition")
+    k, r, n = f["x"].shape[1], f["down"].shape[0], f["up"].shape[0]
+    layer = LowRankLinear(k, n, r).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        layer.down.weight.copy_(to_dev_bf16(f["down"]))
+        layer.up.weight.copy_(to_dev_bf16(f["up"]))
+        y = layer(to_dev_bf16(f["x"]))
+    ok, exact = within_one_ulp(bits_of(y), f["lowrank"], oracle_lib)
+    assert ok and exact > 0.98
+    # and against the oracle's chain on the same inputs
+    ref = oracle_lib.lowrank_up(oracle_lib.lowrank_down(f["x"], f["down"]), f["up"])
+    ok, exact = within_one_ulp(bits_of(y), ref, oracle_lib)
+    assert ok and exact > 0.98
+
+
+def test_rank_padding_is_bitwise_neutral():
+    """Zero rows of down and columns of up add exact zeros: padded and trimmed layers agree bit for bit."""
+    from hyperflow_h3_flash_amd import LowRankLinear, set_lowrank_rank_multiple
+
+    torch.manual_seed(0)
+    layer = LowRankLinear(512, 384, 40).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        layer.down.weight.mul_(0.05)
+        layer.up.weight.mul_(0.05)
+    x = torch.randn(77, 512, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        base = layer(x)
+        assert layer.pad_rank(64)
+        padded = layer(x)
+        holder = torch.nn.Sequential(layer)
+        assert set_lowrank_rank_multiple(holder, 8) == 1 and layer.rank == 40
+        trimmed = layer(x)
+    assert torch.equal(base, padded) and torch.equal(base, trimmed)
+
+
+@pytest.mark.parametrize("rank,bias", [(0, False), (32, True)])
+def test_fused_qkv_is_bitwise_the_three_projections(oracle_lib, rank, bias):
+    from hyperflow_h3_flash_amd import Int8RotLinear, fuse_qkv
+
+    k, g, widths = 1024, 256, (256, 384, 128)
+    rng = np.random.default_rng(rank)
+    layers = []
+    down = torch.randn(rank, k, device=DEV).mul_(0.02).to(torch.bfloat16) if rank else None
+    for n in widths:
+        layer = Int8RotLinear(k, n, g, rank=rank, bias=bias).to(DEV)
+        with torch.no_grad():
+            layer.qweight.copy_(torch.from_numpy(rng.integers(-127, 128, size=(n, k)).astype(np.int8)))
+            layer.wscale.copy_(torch.from_numpy(rng.uniform(1e-3, 1e-2, size=n).astype(np.float32)))
+            if rank:
+                layer.down.weight.copy_(down)
+                layer.up.weight.copy_(torch.randn(n, rank, device=DEV).mul_(0.02))
+            if bias:
+                layer.bias.copy_(torch.randn(n, device=DEV).mul_(0.01))
+        layers.append(layer)
+    fused = fuse_qkv(*layers)
+    x = to_dev_bf16(oracle_lib.make_inputs(300, k, 8, g, seed=rank)["x"])
+    with torch.no_grad():
+        separate = torch.cat([layer(x) for layer in layers], dim=-1)
+        together = fused(x)
+    assert torch.equal(separate, together)

@@ -276,3 +276,26 @@ def test_quantize_weight_against_a_direct_float64_loop(oracle_lib):
                        for kk0 in range(0, 32, 16) for jj in range(16))
             assert abs(float(ws[o]) - amax / 127.0) <= 1e-7 * amax
             assert int(q[o, k0 + j]) == int(np.clip(np.round(rot / (amax / 127.0)), -127, 127))
+
+
+def test_lowrank_up_matches_reference_golden(oracle_lib):
+    """The low-rank branch `up(down(x))` written by the reference's own bf16 modules (the composition fixture):
+    from the golden u, the oracle's exactly rounded sum agrees within one bf16 ulp (torch's CPU bf16 GEMM sums in
+    fp32 in its own order) and bitwise on almost every element."""
+    f = load_fixture("composition")
+    got = oracle_lib.bf16_to_f32(oracle_lib.lowrank_up(f["u"], f["up"]))
+    ref = oracle_lib.bf16_to_f32(f["lowrank"])
+    assert (np.abs(got - ref) <= np.abs(ref) * 2.0**-7).all()
+    assert (got == ref).mean() > 0.99
+
+
+def test_lowrank_up_planted_transpose_is_caught(oracle_lib):
+    """A transposed operand (u @ up instead of u @ up^T on a square case) must not pass the golden check."""
+    f = load_fixture("composition")
+    up = f["up"][:32]  # square 32 x 32 slice
+    right = oracle_lib.bf16_to_f32(oracle_lib.lowrank_up(f["u"], up))
+    wrong = oracle_lib.bf16_to_f32(oracle_lib.f64_to_bf16(
+        oracle_lib.bf16_to_f32(f["u"]).astype(np.float64) @ oracle_lib.bf16_to_f32(up).astype(np.float64)))
+    ref = oracle_lib.bf16_to_f32(f["lowrank"])[:, :32]
+    assert (np.abs(right - ref) <= np.abs(ref) * 2.0**-7).all()
+    assert not (np.abs(wrong - ref) <= np.abs(ref) * 2.0**-7).all()
