@@ -6,6 +6,7 @@
 #include "int8_gemm.hip"
 #include "lowrank.hip"
 #include "rotate_quant.hip"
+#include "splitk.hip"
 
 namespace {
 
@@ -62,9 +63,8 @@ int check_gemm_operands(const int8_t* q, int64_t ldq, const int8_t* w, int64_t l
   return HF_OK;
 }
 
-// Workgroups for the persistent GEMM: one per CU of the current device (queried once per device), at most one per
-// tile.
-int gemm_grid(int64_t tiles) {
+// CUs of the current device (queried once per device).
+int device_cus() {
   static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
@@ -73,14 +73,21 @@ int gemm_grid(int64_t tiles) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     if (dev < 64) cus[dev] = n;
   }
-  return (int)std::min<int64_t>(tiles, n);
+  return n;
 }
+
+// Workgroups for the persistent GEMM: one per CU, at most one per work item.
+int gemm_grid(int64_t items) { return (int)std::min<int64_t>(items, device_cus()); }
 
 int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream) {
   allow_large_lds();
   a.tiles_m = (a.M + hf::GBM - 1) / hf::GBM;
   a.tiles_n = (a.N + hf::GBN - 1) / hf::GBN;
-  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+  if (a.splits <= 0) {
+    a.splits = 1;
+    a.k_chunk = (int)(((int64_t)a.K + hf::GBK - 1) / hf::GBK * hf::GBK);
+  }
+  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n * a.splits;
   if (tiles == 0) return HF_OK;
   if (tiles >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   const dim3 grid((unsigned)gemm_grid(tiles)), block(hf::kThreads);
@@ -93,6 +100,162 @@ int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream) {
   }
   return launch_status();
 }
+
+// Split plan of the low-rank down projection: few row blocks leave most CUs idle, so K is split into chunks of at
+// least 4 stages (256 elements) until the grid covers the CUs; the fp32 partials are tiny (M x r per split).
+struct LrPlan {
+  int splits = 1;
+  int k_chunk = 0;
+};
+
+LrPlan lowrank_plan(int64_t M, int64_t K) {
+  LrPlan p;
+  p.k_chunk = (int)K;
+  const int64_t blocks = (M + hf::kLrRows - 1) / hf::kLrRows;
+  const int64_t stages = (K + hf::kLrStageK - 1) / hf::kLrStageK;
+  const int64_t want = std::min<int64_t>(std::min<int64_t>(device_cus() / std::max<int64_t>(blocks, 1), stages / 4),
+                                         hf::kMaxSplits);
+  if (want >= 2) {
+    const int64_t chunk_stages = (stages + want - 1) / want;
+    p.k_chunk = (int)(chunk_stages * hf::kLrStageK);
+    p.splits = (int)((K + p.k_chunk - 1) / p.k_chunk);
+  }
+  return p;
+}
+
+int64_t lowrank_ws_bytes(int64_t M, int64_t K, int32_t r) {
+  const LrPlan p = lowrank_plan(M, K);
+  return p.splits > 1 ? (int64_t)p.splits * M * r * 4 : 0;
+}
+
+int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_t ld_down, uint16_t* u,
+                      int64_t ldu, int64_t M, int64_t K, int32_t r, void* ws, int64_t ws_bytes,
+                      hf_stream_t stream) {
+  if (M < 0 || K <= 0 || r < 0 || ldx < K || ld_down < K || ldu < r) return HF_ERR_ARGUMENT;
+  if (M == 0 || r == 0) return HF_OK;
+  if (!x || !down || !u) return HF_ERR_ARGUMENT;
+  if (K % 16 || !aligned(x, 16) || !aligned(down, 16) || (ldx % 8) || (ld_down % 8) || !aligned(u, 8))
+    return HF_ERR_ALIGNMENT;
+  if (M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  if (2 * hf::kLrRows * ldx >= (int64_t(1) << 31) || 2 * hf::kLrRanks * ld_down >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  allow_large_lds();
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned blocks = (unsigned)((M + hf::kLrRows - 1) / hf::kLrRows);
+  LrPlan plan = lowrank_plan(M, K);
+  if (plan.splits > 1 && (!ws || ws_bytes < (int64_t)plan.splits * M * std::min<int32_t>(r, hf::kLrRanks) * 4 ||
+                          !aligned(ws, 16))) {
+    plan = LrPlan{};  // no (or too small a) workspace: one pass over K
+    plan.k_chunk = (int)K;
+  }
+  float* part = plan.splits > 1 ? static_cast<float*>(ws) : nullptr;
+  for (int32_t j0 = 0; j0 < r; j0 += hf::kLrRanks) {
+    const int rr = std::min<int32_t>(hf::kLrRanks, r - j0);
+    const uint16_t* d = down + (int64_t)j0 * ld_down;
+    uint16_t* uo = u + j0;
+    const dim3 grid(blocks, (unsigned)plan.splits);
+    if (rr <= 32) {
+      hipLaunchKernelGGL(hf::lowrank_down_kernel<1>, grid, dim3(hf::kLrThreads), hf::kLrLds, s, x, ldx, d, ld_down, uo,
+                         ldu, (int)M, (int)K, rr, plan.k_chunk, part);
+    } else {
+      hipLaunchKernelGGL(hf::lowrank_down_kernel<2>, grid, dim3(hf::kLrThreads), hf::kLrLds, s, x, ldx, d, ld_down, uo,
+                         ldu, (int)M, (int)K, rr, plan.k_chunk, part);
+    }
+    int st = launch_status();
+    if (st != HF_OK) return st;
+    if (part) {
+      const int64_t n = M * rr;
+      hipLaunchKernelGGL(hf::lowrank_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part,
+                         plan.splits, uo, ldu, (int)M, rr);
+      st = launch_status();
+      if (st != HF_OK) return st;
+    }
+  }
+  return HF_OK;
+}
+
+// Split plan of the INT8 GEMM: when the 256 x 256 tiles are fewer than the CUs, K is split so more CUs share the
+// weight stream. A small cost model picks the split: the MFMA time of one round of work items against the memory
+// time of the weight, the activations and the int32 partials (written and read back).
+struct GemmPlan {
+  int splits = 1;
+  int k_chunk = 0;
+};
+
+GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
+  GemmPlan best;
+  const int64_t stages = (K + hf::GBK - 1) / hf::GBK;
+  best.k_chunk = (int)(stages * hf::GBK);
+  const int64_t tiles = ((M + hf::GBM - 1) / hf::GBM) * ((N + hf::GBN - 1) / hf::GBN);
+  const int64_t cus = device_cus();
+  if (tiles >= cus || stages < 4) return best;
+  const double tile_s = 2.0 * hf::GBM * hf::GBN * hf::GBK / (8192.0 * 2.0e9 * 0.55);  // one stage of one tile
+  const double bw = 5.0e12;
+  const double fixed_bytes = (double)N * K + (double)M * K + 2.0 * M * N;
+  double best_t = 1e30;
+  for (int64_t s = 1; s <= std::min<int64_t>(stages / 2, hf::kMaxSplits); ++s) {
+    const int64_t chunk = (stages + s - 1) / s;
+    const int64_t splits = (stages + chunk - 1) / chunk;
+    const double rounds = (double)((tiles * splits + cus - 1) / cus);
+    const double t_mfma = rounds * chunk * tile_s;
+    const double t_mem = (fixed_bytes + (splits > 1 ? 8.0 * splits * M * N : 0.0)) / bw;
+    const double t = std::max(t_mfma, t_mem);
+    if (t < best_t * 0.97) {
+      best_t = t;
+      best.splits = (int)splits;
+      best.k_chunk = (int)(chunk * hf::GBK);
+    }
+  }
+  return best;
+}
+
+int64_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  const GemmPlan p = gemm_plan(M, N, K);
+  const int64_t ld = (N + 3) / 4 * 4;
+  return p.splits > 1 ? (int64_t)p.splits * M * ld * 4 : 0;
+}
+
+int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
+                     const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r,
+                     const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                     int64_t ws_bytes, hf_stream_t stream) {
+  if (M == 0 || N == 0) return (M < 0 || N < 0) ? HF_ERR_ARGUMENT : HF_OK;
+  int st = check_gemm_operands(q, ldq, w, ldw, M, N, K);
+  if (st != HF_OK) return st;
+  if (!sx || !sw || !y || ldy < N || r < 0) return HF_ERR_ARGUMENT;
+  if (!aligned(y, 8)) return HF_ERR_ALIGNMENT;
+  if (r > 0) {
+    if (!u || !up || ldu < r || ld_up < r) return HF_ERR_ARGUMENT;
+    if ((r % 8) || !aligned(u, 16) || !aligned(up, 16) || (ldu % 8) || (ld_up % 8)) return HF_ERR_ALIGNMENT;
+    if (512 * ldu >= (int64_t(1) << 31) || 512 * ld_up >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const GemmPlan plan = gemm_plan(M, N, K);
+  const int64_t ld_acc = (N + 3) / 4 * 4;
+  if (plan.splits > 1 && ws && aligned(ws, 16) && ws_bytes >= (int64_t)plan.splits * M * ld_acc * 4) {
+    // Split K: int32 partial planes, then one pass that adds them and applies the epilogue.
+    hf::GemmArgs a{};
+    a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.out = ws; a.ldo = ld_acc;
+    a.M = (int)M; a.N = (int)N; a.K = (int)K; a.out_vec16 = 1;
+    a.splits = plan.splits; a.k_chunk = plan.k_chunk; a.split_stride = M * ld_acc;
+    st = launch_gemm(a, true, s);
+    if (st != HF_OK) return st;
+    const int64_t tiles_n = (N + hf::kSkTileN - 1) / hf::kSkTileN;
+    const int64_t blocks = ((M + hf::kSkTileM - 1) / hf::kSkTileM) * tiles_n;
+    if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+    const int vec = aligned(y, 8) && (ldy % 4) == 0;
+    hipLaunchKernelGGL(hf::splitk_epilogue_kernel, dim3((unsigned)blocks), dim3(64), 0, s,
+                       static_cast<const int32_t*>(ws), ld_acc, M * ld_acc, plan.splits, sx, sw, r > 0 ? u : nullptr,
+                       ldu, r > 0 ? up : nullptr, ld_up, r, bias, y, ldy, (int)M, (int)N, (int)tiles_n, vec);
+    return launch_status();
+  }
+  hf::GemmArgs a{};
+  a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.sx = sx; a.sw = sw;
+  a.u = r > 0 ? u : nullptr; a.ldu = ldu; a.up = r > 0 ? up : nullptr; a.ldup = ld_up; a.r = r;
+  a.bias = bias; a.out = y; a.ldo = ldy; a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  a.out_vec16 = aligned(y, 16) && (ldy % 8) == 0;
+  return launch_gemm(a, false, s);
+}
+
 
 }  // namespace
 
@@ -140,31 +303,7 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
 
 int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_t ld_down, uint16_t* u,
                     int64_t ldu, int64_t M, int64_t K, int32_t r, hf_stream_t stream) {
-  if (M < 0 || K <= 0 || r < 0 || ldx < K || ld_down < K || ldu < r) return HF_ERR_ARGUMENT;
-  if (M == 0 || r == 0) return HF_OK;
-  if (!x || !down || !u) return HF_ERR_ARGUMENT;
-  if (K % 16 || !aligned(x, 16) || !aligned(down, 16) || (ldx % 8) || (ld_down % 8) || !aligned(u, 8))
-    return HF_ERR_ALIGNMENT;
-  if (M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HF_ERR_SIZE;
-  if (2 * hf::kLrRows * ldx >= (int64_t(1) << 31) || 2 * hf::kLrRanks * ld_down >= (int64_t(1) << 31)) return HF_ERR_SIZE;
-  allow_large_lds();
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned blocks = (unsigned)((M + hf::kLrRows - 1) / hf::kLrRows);
-  for (int32_t j0 = 0; j0 < r; j0 += hf::kLrRanks) {
-    const int rr = std::min<int32_t>(hf::kLrRanks, r - j0);
-    const uint16_t* d = down + (int64_t)j0 * ld_down;
-    uint16_t* uo = u + j0;
-    if (rr <= 32) {
-      hipLaunchKernelGGL(hf::lowrank_down_kernel<1>, dim3(blocks), dim3(hf::kLrThreads), hf::kLrLds, s, x, ldx, d,
-                         ld_down, uo, ldu, (int)M, (int)K, rr);
-    } else {
-      hipLaunchKernelGGL(hf::lowrank_down_kernel<2>, dim3(blocks), dim3(hf::kLrThreads), hf::kLrLds, s, x, ldx, d,
-                         ld_down, uo, ldu, (int)M, (int)K, rr);
-    }
-    const int st = launch_status();
-    if (st != HF_OK) return st;
-  }
-  return HF_OK;
+  return lowrank_down_impl(x, ldx, down, ld_down, u, ldu, M, K, r, nullptr, 0, stream);
 }
 
 int hf_lowrank_up(const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
@@ -189,22 +328,29 @@ int hf_lowrank_up(const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld
 int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
                    const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
                    uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hf_stream_t stream) {
-  if (M == 0 || N == 0) return (M < 0 || N < 0) ? HF_ERR_ARGUMENT : HF_OK;
-  int st = check_gemm_operands(q, ldq, w, ldw, M, N, K);
-  if (st != HF_OK) return st;
-  if (!sx || !sw || !y || ldy < N || r < 0) return HF_ERR_ARGUMENT;
-  if (!aligned(y, 8)) return HF_ERR_ALIGNMENT;
-  if (r > 0) {
-    if (!u || !up || ldu < r || ld_up < r) return HF_ERR_ARGUMENT;
-    if ((r % 8) || !aligned(u, 16) || !aligned(up, 16) || (ldu % 8) || (ld_up % 8)) return HF_ERR_ALIGNMENT;
-    if (512 * ldu >= (int64_t(1) << 31) || 512 * ld_up >= (int64_t(1) << 31)) return HF_ERR_SIZE;
-  }
-  hf::GemmArgs a{};
-  a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.sx = sx; a.sw = sw;
-  a.u = r > 0 ? u : nullptr; a.ldu = ldu; a.up = r > 0 ? up : nullptr; a.ldup = ld_up; a.r = r;
-  a.bias = bias; a.out = y; a.ldo = ldy; a.M = (int)M; a.N = (int)N; a.K = (int)K;
-  a.out_vec16 = aligned(y, 16) && (ldy % 8) == 0;
-  return launch_gemm(a, false, static_cast<hipStream_t>(stream));
+  return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, M, N, K, nullptr, 0, stream);
+}
+
+int64_t hf_int8_linear_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return gemm_ws_bytes(M, N, K);
+}
+
+int hf_int8_linear_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
+                      const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r,
+                      const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                      int64_t ws_bytes, hf_stream_t stream) {
+  return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, M, N, K, ws, ws_bytes, stream);
+}
+
+int64_t hf_lowrank_down_ws_bytes(int64_t M, int64_t K, int32_t r) {
+  if (M <= 0 || K <= 0 || r <= 0) return 0;
+  return lowrank_ws_bytes(M, K, std::min<int32_t>(r, hf::kLrRanks));
+}
+
+int hf_lowrank_down_ws(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_t ld_down, uint16_t* u,
+                       int64_t ldu, int64_t M, int64_t K, int32_t r, void* ws, int64_t ws_bytes, hf_stream_t stream) {
+  return lowrank_down_impl(x, ldx, down, ld_down, u, ldu, M, K, r, ws, ws_bytes, stream);
 }
 
 int hf_int8_gemm_i32(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, int32_t* acc, int64_t ldacc,

@@ -71,6 +71,11 @@ struct GemmArgs {
   int M, N, K;
   int tiles_m, tiles_n;
   int out_vec16;         // bf16 rows may be written 16 bytes at a time (16-byte aligned base and ldo % 8 == 0)
+  // Split K (int32 output only): work item w covers tile w % tiles and K bytes [s * k_chunk, (s + 1) * k_chunk) with
+  // s = w / tiles, and writes its partial accumulators to plane s, split_stride elements after plane s - 1.
+  int splits;            // 1: no split
+  int k_chunk;           // multiple of GBK
+  int64_t split_stride;
 };
 
 // Workgroup id -> (tile_m, tile_n). The dispatcher deals workgroup ids round robin to the 8 XCDs (XCD = id % 8,
@@ -98,14 +103,20 @@ __device__ __forceinline__ int row_swz(int r) { return (r & 7) ^ ((r >> 3) & 3);
 // tile past the last one, read as zero). Wave-uniform: it lives in scalar registers.
 struct TileSrc {
   int m0, n0, rows_m, rows_n;
+  int k_lo, k_hi;  // the work item's K range
+  int split;
   uint32_t bytes_q, bytes_w;
   __amdgpu_buffer_rsrc_t rq, rw;
 };
 
 __device__ __forceinline__ void tile_src(const GemmArgs& a, int id, TileSrc& t) {
   int tm = 0, tn = 0;
-  const bool live = id < a.tiles_m * a.tiles_n;
-  if (live) tile_of(id, a.tiles_m, a.tiles_n, tm, tn);
+  const int tiles = a.tiles_m * a.tiles_n;
+  const bool live = id < tiles * a.splits;
+  t.split = live ? id / tiles : 0;
+  if (live) tile_of(id - t.split * tiles, a.tiles_m, a.tiles_n, tm, tn);
+  t.k_lo = t.split * a.k_chunk;
+  t.k_hi = min(a.K, t.k_lo + a.k_chunk);
   t.m0 = tm * GBM;
   t.n0 = tn * GBN;
   t.rows_m = live ? min(GBM, a.M - t.m0) : 0;
@@ -138,9 +149,9 @@ __device__ __forceinline__ void load_one(const GemmArgs& a, const TileSrc& t, co
   const int row0 = 8 * (kBlkPerWave * wave + i);
   const int row = row0 + ll.lrow;
   const uint32_t cb = ll.chunk ^ (uint32_t)(16 * (i & 3));
-  const uint32_t k0 = (uint32_t)(kt * GBK);
+  const uint32_t k0 = (uint32_t)(t.k_lo + kt * GBK);
   const uint32_t off = (isw ? ll.row_w : ll.row_q) + (uint32_t)(row0 * ld) + cb + k0;
-  const uint32_t voff = ((row < rows_valid) & (k0 + cb < (uint32_t)a.K)) ? off : oob;  // '&': no branch
+  const uint32_t voff = ((row < rows_valid) & (k0 + cb < (uint32_t)t.k_hi)) ? off : oob;  // '&': no branch
   __builtin_amdgcn_raw_ptr_buffer_load_lds(isw ? t.rw : t.rq,
                                            (void HF_LDS*)(slot + (isw ? kAStage : 0) + (row0 / 8) * 1024), 16,
                                            voff, 0, 0, 0);
@@ -237,9 +248,9 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) ca[ks] = sub * GBK + (((2 * ks + half) ^ row_swz(sub)) << 4);
 
-  // K stages per tile, at least 2 (stages past K read zeros and add nothing).
-  const int nk = max((a.K + GBK - 1) / GBK, 2);
-  const int total = a.tiles_m * a.tiles_n;
+  // K stages per work item, at least 2 (stages past its K range read zeros and add nothing).
+  const int nk = max((a.k_chunk + GBK - 1) / GBK, 2);
+  const int total = a.tiles_m * a.tiles_n * a.splits;
   int id = blockIdx.x;
   LaneLoad ll;
   ll.lrow = lane >> 3;
@@ -376,7 +387,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     bool full;
     if constexpr (OUT == kOutI32) {
       full = cur.rows_m == GBM && cur.rows_n == GBN && a.out_vec16;
-      int32_t* out = static_cast<int32_t*>(a.out);
+      int32_t* out = static_cast<int32_t*>(a.out) + cur.split * a.split_stride;
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         const int m = m0 + wm * 128 + jb * 32 + esub;
@@ -390,8 +401,12 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
             if (full) {
               *reinterpret_cast<v4i*>(dst) = (v4i){c[4 * gq], c[4 * gq + 1], c[4 * gq + 2], c[4 * gq + 3]};
             } else if (m < a.M) {
-              for (int e = 0; e < 4; ++e)
-                if (n + e < a.N) dst[e] = c[4 * gq + e];
+              if (a.out_vec16 && n + 4 <= a.N) {
+                *reinterpret_cast<v4i*>(dst) = (v4i){c[4 * gq], c[4 * gq + 1], c[4 * gq + 2], c[4 * gq + 3]};
+              } else {
+                for (int e = 0; e < 4; ++e)
+                  if (n + e < a.N) dst[e] = c[4 * gq + e];
+              }
             }
           }
       }

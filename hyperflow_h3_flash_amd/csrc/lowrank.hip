@@ -42,11 +42,15 @@ __device__ __forceinline__ void lr_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t oo
   }
 }
 
+// Split K (few rows): blockIdx.y = s covers K elements [s * k_chunk, (s + 1) * k_chunk) and writes its fp32 partial
+// sums to plane s of `part` ([splits][M][r]); lowrank_reduce_kernel adds the planes and rounds to bf16. Unsplit
+// launches (gridDim.y == 1, part == nullptr) write u directly.
 template <int RB>
 __global__ __launch_bounds__(kLrThreads, 1) void lowrank_down_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                      const uint16_t* __restrict__ down, int64_t ldd,
                                                                      uint16_t* __restrict__ u, int64_t ldu, int M,
-                                                                     int K, int r) {
+                                                                     int K, int r, int k_chunk,
+                                                                     float* __restrict__ part) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lr_smem_raw[];
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)lr_smem_raw;
   const int lane = threadIdx.x & 63;
@@ -55,24 +59,26 @@ __global__ __launch_bounds__(kLrThreads, 1) void lowrank_down_kernel(const uint1
   const int m0 = blockIdx.x * kLrRows;
   const int rows_m = min(kLrRows, M - m0);
 
+  const int k_lo = blockIdx.y * k_chunk;
+  const int k_len = min(K - k_lo, k_chunk);
   const uint32_t ldx_bytes = (uint32_t)ldx * 2u, ldd_bytes = (uint32_t)ldd * 2u;
   const uint32_t bytes_x = (uint32_t)rows_m * ldx_bytes, bytes_d = (uint32_t)r * ldd_bytes;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (int64_t)m0 * ldx, bytes_x);
-  const __amdgpu_buffer_rsrc_t rd = make_rsrc(down, bytes_d);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (int64_t)m0 * ldx + k_lo, bytes_x - 2u * (uint32_t)k_lo);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(down + k_lo, bytes_d - 2u * (uint32_t)k_lo);
 
   // Stage t -> slot t % kLrStages; every stage issues 6 loads per wave (4 of x, 2 of down), stages past the end
   // load zeros, so "stage t has landed" is always vmcnt(24) with the four later stages in flight.
   auto issue = [&](int t) {
     unsigned char HF_LDS* st = smem + (t % kLrStages) * kLrStageBytes;
-    lr_load<4>(rx, bytes_x, ldx_bytes, rows_m, t * kLrStageK, K, st, wave * 4, lane);
-    lr_load<2>(rd, bytes_d, ldd_bytes, r, t * kLrStageK, K, st + kLrXBytes, wave * 2, lane);
+    lr_load<4>(rx, bytes_x, ldx_bytes, rows_m, t * kLrStageK, k_len, st, wave * 4, lane);
+    lr_load<2>(rd, bytes_d, ldd_bytes, r, t * kLrStageK, k_len, st + kLrXBytes, wave * 2, lane);
   };
 
   v16f acc[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) acc[rb] = (v16f){0};
 
-  const int nst = (K + kLrStageK - 1) / kLrStageK;
+  const int nst = (k_len + kLrStageK - 1) / kLrStageK;
 #pragma unroll
   for (int t = 0; t < kLrStages - 1; ++t) issue(t);
   const int xrow = wave * 32 + sub;
@@ -99,6 +105,19 @@ __global__ __launch_bounds__(kLrThreads, 1) void lowrank_down_kernel(const uint1
 
   const int row = m0 + xrow;
   if (row >= M) return;
+  if (part) {
+    float* dst = part + ((int64_t)blockIdx.y * M + row) * r;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = rb * 32 + 8 * g + 4 * half + e;
+          if (j < r) dst[j] = acc[rb][4 * g + e];
+        }
+    return;
+  }
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
@@ -117,9 +136,28 @@ __global__ __launch_bounds__(kLrThreads, 1) void lowrank_down_kernel(const uint1
 }
 
 template __global__ void lowrank_down_kernel<1>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
-                                                int64_t, int, int, int);
+                                                int64_t, int, int, int, int, float*);
 template __global__ void lowrank_down_kernel<2>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
-                                                int64_t, int, int, int);
+                                                int64_t, int, int, int, int, float*);
+
+constexpr int kMaxSplits = 32;  // K chunks of a split launch, at most
+
+// u[m, j] = bf16(sum_s part[s][m][j]): the planes added in a fixed order, one rounding (round to nearest even).
+__global__ __launch_bounds__(256) void lowrank_reduce_kernel(const float* __restrict__ part, int splits,
+                                                             uint16_t* __restrict__ u, int64_t ldu, int M, int r) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)M * r) return;
+  const int m = (int)(i / r), j = (int)(i % r);
+  // All loads first (splits <= kMaxSplits), then the adds in plane order.
+  float p[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) p[s] = s < splits ? part[(int64_t)s * M * r + i] : 0.0f;
+  float v = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s)
+    if (s < splits) v += p[s];
+  u[(int64_t)m * ldu + j] = (uint16_t)f32_to_bf16_rne(v);
+}
 
 // Low-rank up projection y = bf16(u @ up^T + bias), the second half of LowRankLinear.forward
 // (src/hyperflow_h3_flash/transformer.py:57-58: `self.up(...)`, a bias-free bf16 nn.Linear; the bias is this build's

@@ -180,6 +180,13 @@ def _stream(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def _workspace(device: torch.device, nbytes: int) -> tuple[Tensor | None, int]:
+    """A device workspace of ``nbytes`` (None for 0) from torch's caching allocator; the kernels never allocate."""
+    if nbytes <= 0:
+        return None, 0
+    return torch.empty(nbytes, device=device, dtype=torch.uint8), nbytes
+
+
 def _check(status: int, what: str) -> None:
     if status == _native.HF_OK:
         return
@@ -217,10 +224,12 @@ def lowrank_down(x: Tensor, down: Tensor) -> Tensor:
     _same_device(x.device, down)
     down = down.to(torch.bfloat16).contiguous()
     u = torch.empty(M, r, device=x.device, dtype=torch.bfloat16)
+    lib = _native.library()
     with torch.cuda.device(x.device):
-        status = _native.library().hf_lowrank_down(_ptr(x), x.stride(0), _ptr(down), down.stride(0), _ptr(u),
-                                                   u.stride(0), M, K, r, _stream(x.device))
-    _check(status, "hf_lowrank_down")
+        ws, nbytes = _workspace(x.device, lib.hf_lowrank_down_ws_bytes(M, K, r))
+        status = lib.hf_lowrank_down_ws(_ptr(x), x.stride(0), _ptr(down), down.stride(0), _ptr(u), u.stride(0), M, K,
+                                        r, _ptr(ws), nbytes, _stream(x.device))
+    _check(status, "hf_lowrank_down_ws")
     return u
 
 
@@ -270,12 +279,14 @@ def int8_matmul(a: Tensor, b: Tensor, sa: Tensor, sb: Tensor, *, u: Tensor | Non
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
     c = torch.empty(M, N, device=a.device, dtype=torch.bfloat16)
+    lib = _native.library()
     with torch.cuda.device(a.device):
-        status = _native.library().hf_int8_linear(
+        ws, nbytes = _workspace(a.device, lib.hf_int8_linear_ws_bytes(M, N, K))
+        status = lib.hf_int8_linear_ws(
             _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(sa), _ptr(sb),
             _ptr(u), u.stride(0) if u is not None else 0, _ptr(up), up.stride(0) if up is not None else 0, r,
-            _ptr(bias), _ptr(c), c.stride(0), M, N, K, _stream(a.device))
-    _check(status, "hf_int8_linear")
+            _ptr(bias), _ptr(c), c.stride(0), M, N, K, _ptr(ws), nbytes, _stream(a.device))
+    _check(status, "hf_int8_linear_ws")
     return c
 
 

@@ -63,6 +63,16 @@ int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_
                     int64_t ldu, int64_t M, int64_t K, int32_t r, hf_stream_t stream);
 
 /*
+ * hf_lowrank_down with a caller-provided workspace: with few rows the kernel splits K across workgroups (fp32
+ * partial sums in `ws`, added in a fixed order and rounded once to bf16). `hf_lowrank_down_ws_bytes` gives the bytes
+ * it uses for these sizes (0: no split); a NULL or smaller workspace runs the unsplit kernel.
+ * Replaces the same reference interface as hf_lowrank_down (transformer.py:57-58).
+ */
+int64_t hf_lowrank_down_ws_bytes(int64_t M, int64_t K, int32_t r);
+int hf_lowrank_down_ws(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_t ld_down, uint16_t* u,
+                       int64_t ldu, int64_t M, int64_t K, int32_t r, void* ws, int64_t ws_bytes, hf_stream_t stream);
+
+/*
  * Low-rank up projection y = bf16(u @ up^T [+ bias]) (LowRankLinear.up, a bias-free bf16 nn.Linear,
  * transformer.py:57-58; the bias is an extension, NULL for none). Together with hf_lowrank_down this is the whole
  * LowRankLinear forward. fp32 accumulation over the rank, one rounding to bf16 (round to nearest even).
@@ -87,6 +97,19 @@ int hf_lowrank_up(const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld
 int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
                    const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
                    uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hf_stream_t stream);
+
+/*
+ * hf_int8_linear with a caller-provided workspace (16-byte aligned): when the output has fewer 256 x 256 tiles than
+ * the device has CUs (few rows), K is split across workgroups; their int32 partial accumulators (`ws`) are added
+ * exactly and the same epilogue is applied, so the result equals hf_int8_linear's bit for bit.
+ * `hf_int8_linear_ws_bytes` gives the bytes used for these sizes (0: no split); a NULL or smaller workspace runs
+ * the unsplit kernel. Replaces the same reference interface as hf_int8_linear (int8.py:376-390).
+ */
+int64_t hf_int8_linear_ws_bytes(int64_t M, int64_t N, int64_t K);
+int hf_int8_linear_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
+                      const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r,
+                      const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
+                      int64_t ws_bytes, hf_stream_t stream);
 
 /*
  * The int32 accumulator alone: acc = q @ w^T (for parity checks). acc: int32 [M, ldacc], 16-byte aligned.

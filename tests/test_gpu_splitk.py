@@ -1,0 +1,111 @@
+"""Few-row shapes: the split-K GEMM (int32 partial planes + the epilogue pass) and the split-K low-rank down
+projection against the unsplit kernels and the oracle.
+
+Bars: the split GEMM bitwise equal to the unsplit one (integer partial sums add exactly; the epilogue is the same
+arithmetic in the same order), and bitwise equal to the oracle without a low-rank branch or bias; the split
+low-rank down projection within one bf16 ulp of the oracle (fp32 sums in another order) and bitwise on almost every
+element.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    if not torch.cuda.is_available():
+        pytest.fail("no ROCm device visible")
+    from hyperflow_h3_flash_amd import _native
+
+    _native.library()
+
+
+def to_dev_bf16(bits: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def bits_of(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def run_linear(lib, q, w, sx, ws, u, up, bias, split):
+    m, k = q.shape
+    n = w.shape[0]
+    r = 0 if u is None else u.shape[1]
+    y = torch.full((m, n), -1, device=DEV, dtype=torch.int16).view(torch.bfloat16)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    args = (p(q), k, p(w), k, p(sx), p(ws), p(u), r if r else 0, p(up), r if r else 0, r, p(bias), p(y), n, m, n, k)
+    if split:
+        nbytes = lib.hf_int8_linear_ws_bytes(m, n, k)
+        assert nbytes > 0, "this shape should take the split path"
+        work = torch.empty(nbytes, device=DEV, dtype=torch.uint8)
+        status = lib.hf_int8_linear_ws(*args, p(work), nbytes, stream)
+    else:
+        status = lib.hf_int8_linear(*args, stream)
+    assert status == 0
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("m,n,k,r,bias", [(1, 5120, 5120, 0, False), (64, 5120, 5120, 0, False),
+                                          (64, 5000, 5120, 32, True), (200, 3072, 3072, 64, False),
+                                          (37, 1000, 2048, 136, True), (256, 5120, 5120, 32, False)])
+def test_split_gemm_is_bitwise_the_unsplit_gemm(oracle_lib, m, n, k, r, bias):
+    from hyperflow_h3_flash_amd import _native
+    from hyperflow_h3_flash_amd.int8 import rotate_quant
+
+    lib = _native.library()
+    inp = oracle_lib.make_inputs(m, k, n, 256, rank=r, bias=bias, seed=m + n + r)
+    x = to_dev_bf16(inp["x"])
+    q, sx = rotate_quant(x, 256)
+    w = torch.from_numpy(inp["qweight"]).to(DEV)
+    ws = torch.from_numpy(inp["wscale"]).to(DEV)
+    u = up = b = None
+    if r:
+        from hyperflow_h3_flash_amd.int8 import lowrank_down
+
+        u = lowrank_down(x, to_dev_bf16(inp["down"]))
+        up = to_dev_bf16(inp["up"])
+    if bias:
+        b = to_dev_bf16(inp["bias"])
+    split = run_linear(lib, q, w, sx, ws, u, up, b, True)
+    whole = run_linear(lib, q, w, sx, ws, u, up, b, False)
+    assert torch.equal(split.view(torch.int16), whole.view(torch.int16))
+    if not r and not bias:
+        ref = oracle_lib.convrot_linear(inp["x"], inp["qweight"], inp["wscale"], 256)
+        np.testing.assert_array_equal(bits_of(split), ref["y"])
+
+
+@pytest.mark.parametrize("m,k,r", [(1, 5120, 32), (64, 5120, 64), (100, 13824, 32), (300, 5120, 136)])
+def test_split_lowrank_down_matches_oracle(oracle_lib, m, k, r):
+    from hyperflow_h3_flash_amd import _native
+    from hyperflow_h3_flash_amd.int8 import lowrank_down
+
+    assert _native.library().hf_lowrank_down_ws_bytes(m, k, r) > 0, "this shape should take the split path"
+    inp = oracle_lib.make_inputs(m, k, 8, 256, rank=r, seed=k + r)
+    u = lowrank_down(to_dev_bf16(inp["x"]), to_dev_bf16(inp["down"]))
+    got = oracle_lib.bf16_to_f32(bits_of(u))
+    ref = oracle_lib.bf16_to_f32(oracle_lib.lowrank_down(inp["x"], inp["down"]))
+    assert (np.abs(got - ref) <= np.abs(ref) * 2.0**-7 + 1e-7).all()
+    assert (got == ref).mean() > 0.99
+
+
+def test_large_shapes_do_not_split():
+    from hyperflow_h3_flash_amd import _native
+
+    lib = _native.library()
+    assert lib.hf_int8_linear_ws_bytes(32768, 15360, 5120) == 0
+    assert lib.hf_lowrank_down_ws_bytes(32768, 5120, 64) == 0
