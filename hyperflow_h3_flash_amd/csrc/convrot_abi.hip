@@ -6,11 +6,14 @@
 #include "int8_gemm.hip"
 #include "lowrank.hip"
 #include "rotate_quant.hip"
+#include "skinny.hip"
 #include "splitk.hip"
 
 namespace {
 
 constexpr int kMaxLds = 160 * 1024;
+// Rows up to which the rotation runs one workgroup per row (every tile of a row in flight at once).
+constexpr int64_t kRowKernelMaxRows = 1024;
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
@@ -44,12 +47,22 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<4>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<1>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<2>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<3>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<4>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<1>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLrLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<2>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLrLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_up_kernel),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kUpLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kSkinnyLds);
     (void)hipGetLastError();
   });
 }
@@ -179,10 +192,23 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
 struct GemmPlan {
   int splits = 1;
   int k_chunk = 0;
+  bool skinny = false;  // at most 64 rows: 128-row weight slices (skinny_gemm_kernel) instead of 256 x 256 tiles
 };
 
 GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
   GemmPlan best;
+  if (M <= hf::kSkinnyM) {
+    // Enough 128-row x K-chunk work items for two per CU, each chunk at least 4 stages (512 bytes of K).
+    const int64_t stages = (K + hf::kSkinnyStageK - 1) / hf::kSkinnyStageK;
+    const int64_t ntiles = (N + hf::kSkinnyN - 1) / hf::kSkinnyN;
+    int64_t want = (2 * device_cus() + ntiles - 1) / ntiles;
+    want = std::max<int64_t>(1, std::min<int64_t>(want, std::min<int64_t>(stages / 4, hf::kMaxSplits)));
+    const int64_t chunk = (stages + want - 1) / want;
+    best.skinny = true;
+    best.k_chunk = (int)(chunk * hf::kSkinnyStageK);
+    best.splits = (int)((stages + chunk - 1) / chunk);
+    return best;
+  }
   const int64_t stages = (K + hf::GBK - 1) / hf::GBK;
   best.k_chunk = (int)(stages * hf::GBK);
   const int64_t tiles = ((M + hf::GBM - 1) / hf::GBM) * ((N + hf::GBN - 1) / hf::GBN);
@@ -211,7 +237,7 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
 int64_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
   const GemmPlan p = gemm_plan(M, N, K);
   const int64_t ld = (N + 3) / 4 * 4;
-  return p.splits > 1 ? (int64_t)p.splits * M * ld * 4 : 0;
+  return (p.splits > 1 || p.skinny) ? (int64_t)p.splits * M * ld * 4 : 0;
 }
 
 int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
@@ -231,13 +257,22 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const GemmPlan plan = gemm_plan(M, N, K);
   const int64_t ld_acc = (N + 3) / 4 * 4;
-  if (plan.splits > 1 && ws && aligned(ws, 16) && ws_bytes >= (int64_t)plan.splits * M * ld_acc * 4) {
+  if ((plan.splits > 1 || plan.skinny) && ws && aligned(ws, 16) &&
+      ws_bytes >= (int64_t)plan.splits * M * ld_acc * 4) {
     // Split K: int32 partial planes, then one pass that adds them and applies the epilogue.
-    hf::GemmArgs a{};
-    a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.out = ws; a.ldo = ld_acc;
-    a.M = (int)M; a.N = (int)N; a.K = (int)K; a.out_vec16 = 1;
-    a.splits = plan.splits; a.k_chunk = plan.k_chunk; a.split_stride = M * ld_acc;
-    st = launch_gemm(a, true, s);
+    if (plan.skinny) {
+      allow_large_lds();
+      const dim3 grid((unsigned)((N + hf::kSkinnyN - 1) / hf::kSkinnyN), (unsigned)plan.splits);
+      hipLaunchKernelGGL(hf::skinny_gemm_kernel, grid, dim3(256), hf::kSkinnyLds, s, q, ldq, w, ldw,
+                         static_cast<int32_t*>(ws), ld_acc, M * ld_acc, (int)M, (int)N, (int)K, plan.k_chunk);
+      st = launch_status();
+    } else {
+      hf::GemmArgs a{};
+      a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.out = ws; a.ldo = ld_acc;
+      a.M = (int)M; a.N = (int)N; a.K = (int)K; a.out_vec16 = 1;
+      a.splits = plan.splits; a.k_chunk = plan.k_chunk; a.split_stride = M * ld_acc;
+      st = launch_gemm(a, true, s);
+    }
     if (st != HF_OK) return st;
     const int64_t tiles_n = (N + hf::kSkTileN - 1) / hf::kSkTileN;
     const int64_t blocks = ((M + hf::kSkTileM - 1) / hf::kSkTileM) * tiles_n;
@@ -288,10 +323,23 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
     waves >>= 1;
   if (waves == 0 || K > 77312) return HF_ERR_SIZE;
   allow_large_lds();
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t ntiles = (K + hf::kRqTile - 1) / hf::kRqTile;
+  if (M <= kRowKernelMaxRows && ntiles <= 14 && M < (int64_t(1) << 31)) {
+    // Few rows: one workgroup per row, one wave per tile.
+    const size_t lds = hf::rotate_quant_row_lds_bytes((int)K);
+    const dim3 grid((unsigned)M), block((unsigned)(64 * ntiles));
+    switch (lg) {
+      case 1: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<1>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
+      case 2: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<2>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
+      case 3: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<3>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
+      default: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<4>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
+    }
+    return launch_status();
+  }
   const size_t lds = hf::rotate_quant_lds_bytes(waves, (int)K);
   const int64_t blocks64 = (M + waves - 1) / waves;
   const unsigned blocks = (unsigned)std::min<int64_t>(blocks64, int64_t(1) << 30);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   switch (lg) {
     case 1: hipLaunchKernelGGL(hf::rotate_quant_kernel<1>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
     case 2: hipLaunchKernelGGL(hf::rotate_quant_kernel<2>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;

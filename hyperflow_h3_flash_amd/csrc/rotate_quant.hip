@@ -53,6 +53,136 @@ __device__ __forceinline__ float quotient(float a, float d, float inv) {
 
 size_t rotate_quant_lds_bytes(int waves, int K) { return (size_t)waves * (kRqScratchBytes + 2 * (size_t)K); }
 
+// Rotates tile t of a row (elements 1024t .. 1024t + 1023; this lane's 16 consecutive inputs in cur0, cur1), rounds
+// every value once to bf16 and parks the bf16 bits in `rowbuf` (the row's buffer) at their natural positions.
+// Returns this lane's absmax of the rounded, still unnormalised sums. `scratch` is the wave's fp64 transpose area.
+template <int LOG4G>
+__device__ __forceinline__ float rotate_tile(uint4 cur0, uint4 cur1, int t, int K, int lane, double* scratch,
+                                             uint16_t* rowbuf) {
+  const int e0 = t * kRqTile + lane * 16;
+  float amax = 0.0f;
+  double v[16];
+  const uint32_t w[8] = {cur0.x, cur0.y, cur0.z, cur0.w, cur1.x, cur1.y, cur1.z, cur1.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[2 * i] = (double)bf16_lo(w[i]);
+    v[2 * i + 1] = (double)bf16_hi(w[i]);
+  }
+  if constexpr (LOG4G >= 1) h4_stage<1>(v);
+  if constexpr (LOG4G >= 2) h4_stage<4>(v);
+
+  if constexpr (LOG4G <= 2) {
+    // Values are in natural order: round, track the absmax, park 16 bf16 in the row buffer.
+    uint32_t packed[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float lo = round_f64_to_bf16_value(v[2 * i]);
+      float hi = round_f64_to_bf16_value(v[2 * i + 1]);
+      amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
+      packed[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+    }
+    if (e0 < K) {
+      uint4* dst = reinterpret_cast<uint4*>(rowbuf + e0);
+      dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+      dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    }
+  } else {
+    // Transpose the fp64 pencils through LDS so each lane holds 16 values along digits 2 (and 3).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      double2 pr;
+      pr.x = v[2 * i];
+      pr.y = v[2 * i + 1];
+      *reinterpret_cast<double2*>(scratch + lane * kRqStride + 2 * i) = pr;
+    }
+    wave_lds_sync();
+    int base_elem;
+    bool valid;
+    if constexpr (LOG4G == 4) {
+      // lane = 16*gi + b; v[a] = pencil (16*gi + a), column b; element 256*gi + 16*a + b
+      const int gi = lane >> 4, b = lane & 15;
+#pragma unroll
+      for (int a = 0; a < 16; ++a) v[a] = scratch[(16 * gi + a) * kRqStride + b];
+      base_elem = t * kRqTile + 256 * gi + b;
+      valid = t * kRqTile + 256 * gi < K;
+      h4_stage<1>(v);
+      h4_stage<4>(v);
+    } else {
+      // lane = 4*gi + cq; v[4a + cc] = pencil (4*gi + a), column 4*cq + cc; element 64*gi + 16*a + 4*cq + cc
+      const int gi = lane >> 2, cq = lane & 3;
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) v[4 * a + cc] = scratch[(4 * gi + a) * kRqStride + 4 * cq + cc];
+      base_elem = t * kRqTile + 64 * gi + 4 * cq;
+      valid = t * kRqTile + 64 * gi < K;
+      h4_stage<4>(v);
+    }
+    wave_lds_sync();  // scratch is rewritten by the next tile
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float r = round_f64_to_bf16_value(v[i]);
+      amax = fmaxf(amax, fabsf(r));
+      if (valid) {
+        const int e = (LOG4G == 4) ? base_elem + 16 * i : base_elem + 16 * (i >> 2) + (i & 3);
+        rowbuf[e] = (uint16_t)(__float_as_uint(r) >> 16);
+      }
+    }
+  }
+  return amax;
+}
+
+// The row's scale and its quotient helpers from the absmax of the unnormalised rounded sums: amax of xr = amax *
+// 2^-n (exact); then the reference's clamp and division (int8.py:177).
+struct RowScale {
+  float sx, d, inv;
+};
+
+template <int LOG4G>
+__device__ __forceinline__ RowScale row_scale(float amax) {
+  RowScale r;
+  r.sx = fmaxf(ldexpf(amax, -LOG4G), 1e-12f) / 127.0f;
+  r.d = ldexpf(r.sx, LOG4G);  // (t * 2^n) / (sx * 2^n) == xr / sx exactly
+  r.inv = 1.0f / r.d;         // correctly rounded; the per-element quotients use it
+  return r;
+}
+
+// Quantizes this lane's 16 elements of tile t from the row buffer (int8.py:178) and writes them (16 bytes).
+__device__ __forceinline__ void quantize_tile(const uint16_t* rowbuf, int t, int K, int lane, const RowScale& rs,
+                                              int8_t* qrow) {
+  const int e0 = t * kRqTile + lane * 16;
+  if (e0 >= K) return;
+  const uint4* src = reinterpret_cast<const uint4*>(rowbuf + e0);
+  const uint4 a = src[0], b = src[1];
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t pair = w[2 * i + h];
+      float r0 = rintf(quotient(bf16_lo(pair), rs.d, rs.inv));
+      float r1 = rintf(quotient(bf16_hi(pair), rs.d, rs.inv));
+      r0 = fminf(fmaxf(r0, -127.0f), 127.0f);
+      r1 = fminf(fmaxf(r1, -127.0f), 127.0f);
+      word |= ((uint32_t)((int)r0 & 0xff) | ((uint32_t)((int)r1 & 0xff) << 8)) << (16 * h);
+    }
+    out[i] = word;
+  }
+  *reinterpret_cast<uint4*>(qrow + e0) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+__device__ __forceinline__ void load_pencil(const uint16_t* xrow, int e, int K, uint4& a, uint4& b) {
+  a = make_uint4(0, 0, 0, 0);
+  b = a;
+  if (e < K) {
+    a = *reinterpret_cast<const uint4*>(xrow + e);
+    b = *reinterpret_cast<const uint4*>(xrow + e + 8);
+  }
+}
+
+// Many rows: one wave per row, walking the row's tiles with the next tile's loads in flight.
 template <int LOG4G>
 __global__ __launch_bounds__(256) void rotate_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                            int8_t* __restrict__ q, int64_t ldq,
@@ -69,133 +199,60 @@ __global__ __launch_bounds__(256) void rotate_quant_kernel(const uint16_t* __res
   for (int64_t row = (int64_t)blockIdx.x * waves + wave; row < M; row += (int64_t)gridDim.x * waves) {
     const uint16_t* xrow = x + row * ldx;
     float amax = 0.0f;
-
-    uint4 nxt0 = make_uint4(0, 0, 0, 0), nxt1 = nxt0;
-    if (lane * 16 < K) {
-      nxt0 = *reinterpret_cast<const uint4*>(xrow + lane * 16);
-      nxt1 = *reinterpret_cast<const uint4*>(xrow + lane * 16 + 8);
-    }
+    uint4 nxt0, nxt1;
+    load_pencil(xrow, lane * 16, K, nxt0, nxt1);
     for (int t = 0; t < ntiles; ++t) {
-      const int e0 = t * kRqTile + lane * 16;
       const uint4 cur0 = nxt0, cur1 = nxt1;
-      if (t + 1 < ntiles) {
-        const int e1 = e0 + kRqTile;
-        nxt0 = make_uint4(0, 0, 0, 0);
-        nxt1 = nxt0;
-        if (e1 < K) {
-          nxt0 = *reinterpret_cast<const uint4*>(xrow + e1);
-          nxt1 = *reinterpret_cast<const uint4*>(xrow + e1 + 8);
-        }
-      }
-      double v[16];
-      const uint32_t w[8] = {cur0.x, cur0.y, cur0.z, cur0.w, cur1.x, cur1.y, cur1.z, cur1.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        v[2 * i] = (double)bf16_lo(w[i]);
-        v[2 * i + 1] = (double)bf16_hi(w[i]);
-      }
-      if constexpr (LOG4G >= 1) h4_stage<1>(v);
-      if constexpr (LOG4G >= 2) h4_stage<4>(v);
-
-      if constexpr (LOG4G <= 2) {
-        // Values are in natural order: round, track the absmax, park 16 bf16 in the row buffer.
-        uint32_t packed[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          float lo = round_f64_to_bf16_value(v[2 * i]);
-          float hi = round_f64_to_bf16_value(v[2 * i + 1]);
-          amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
-          packed[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
-        }
-        if (e0 < K) {
-          uint4* dst = reinterpret_cast<uint4*>(rowbuf + e0);
-          dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-          dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-        }
-      } else {
-        // Transpose the fp64 pencils through LDS so each lane holds 16 values along digits 2 (and 3).
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          double2 pr;
-          pr.x = v[2 * i];
-          pr.y = v[2 * i + 1];
-          *reinterpret_cast<double2*>(scratch + lane * kRqStride + 2 * i) = pr;
-        }
-        wave_lds_sync();
-        int base_elem;
-        bool valid;
-        if constexpr (LOG4G == 4) {
-          // lane = 16*gi + b; v[a] = pencil (16*gi + a), column b; element 256*gi + 16*a + b
-          const int gi = lane >> 4, b = lane & 15;
-#pragma unroll
-          for (int a = 0; a < 16; ++a) v[a] = scratch[(16 * gi + a) * kRqStride + b];
-          base_elem = t * kRqTile + 256 * gi + b;
-          valid = t * kRqTile + 256 * gi < K;
-          h4_stage<1>(v);
-          h4_stage<4>(v);
-        } else {
-          // lane = 4*gi + cq; v[4a + cc] = pencil (4*gi + a), column 4*cq + cc; element 64*gi + 16*a + 4*cq + cc
-          const int gi = lane >> 2, cq = lane & 3;
-#pragma unroll
-          for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) v[4 * a + cc] = scratch[(4 * gi + a) * kRqStride + 4 * cq + cc];
-          base_elem = t * kRqTile + 64 * gi + 4 * cq;
-          valid = t * kRqTile + 64 * gi < K;
-          h4_stage<4>(v);
-        }
-        wave_lds_sync();  // scratch is rewritten by the next tile
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float r = round_f64_to_bf16_value(v[i]);
-          amax = fmaxf(amax, fabsf(r));
-          if (valid) {
-            const int e = (LOG4G == 4) ? base_elem + 16 * i : base_elem + 16 * (i >> 2) + (i & 3);
-            rowbuf[e] = (uint16_t)(__float_as_uint(r) >> 16);
-          }
-        }
-      }
+      if (t + 1 < ntiles) load_pencil(xrow, (t + 1) * kRqTile + lane * 16, K, nxt0, nxt1);
+      amax = fmaxf(amax, rotate_tile<LOG4G>(cur0, cur1, t, K, lane, scratch, rowbuf));
     }
-
-    amax = wave_max(amax);
-    // amax of xr = amax of the unnormalised sums * 2^-n (exact); then the reference's clamp and division.
-    const float sx = fmaxf(ldexpf(amax, -LOG4G), 1e-12f) / 127.0f;
-    const float d = ldexpf(sx, LOG4G);  // (t * 2^n) / (sx * 2^n) == xr / sx exactly
-    const float inv = 1.0f / d;         // correctly rounded; the per-element quotients below use it
-    if (lane == 0) s[row] = sx;
+    const RowScale rs = row_scale<LOG4G>(wave_max(amax));
+    if (lane == 0) s[row] = rs.sx;
     wave_lds_sync();
-
     int8_t* qrow = q + row * ldq;
-    for (int t = 0; t < ntiles; ++t) {
-      const int e0 = t * kRqTile + lane * 16;
-      if (e0 >= K) continue;
-      const uint4* src = reinterpret_cast<const uint4*>(rowbuf + e0);
-      const uint4 a = src[0], b = src[1];
-      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      uint32_t out[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t pair = w[2 * i + h];
-          float r0 = rintf(quotient(bf16_lo(pair), d, inv));
-          float r1 = rintf(quotient(bf16_hi(pair), d, inv));
-          r0 = fminf(fmaxf(r0, -127.0f), 127.0f);
-          r1 = fminf(fmaxf(r1, -127.0f), 127.0f);
-          word |= ((uint32_t)((int)r0 & 0xff) | ((uint32_t)((int)r1 & 0xff) << 8)) << (16 * h);
-        }
-        out[i] = word;
-      }
-      *reinterpret_cast<uint4*>(qrow + e0) = make_uint4(out[0], out[1], out[2], out[3]);
-    }
+    for (int t = 0; t < ntiles; ++t) quantize_tile(rowbuf, t, K, lane, rs, qrow);
     wave_lds_sync();  // the row buffer is rewritten by the next row
   }
+}
+
+// Few rows: one workgroup per row, one wave per 1024-element tile (the whole row's loads in flight at once); the
+// row's absmax goes through LDS. Same arithmetic as rotate_quant_kernel.
+size_t rotate_quant_row_lds_bytes(int K) {
+  const int ntiles = (K + kRqTile - 1) / kRqTile;
+  return (size_t)ntiles * kRqScratchBytes + 2 * (size_t)ntiles * kRqTile + 64 * sizeof(float);
+}
+
+template <int LOG4G>
+__global__ __launch_bounds__(1024) void rotate_quant_row_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                int8_t* __restrict__ q, int64_t ldq,
+                                                                float* __restrict__ s, int K) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int t = threadIdx.x >> 6;  // this wave's tile
+  const int ntiles = blockDim.x >> 6;
+  double* scratch = reinterpret_cast<double*>(smem + (size_t)t * kRqScratchBytes);
+  uint16_t* rowbuf = reinterpret_cast<uint16_t*>(smem + (size_t)ntiles * kRqScratchBytes);
+  float* maxes = reinterpret_cast<float*>(smem + (size_t)ntiles * kRqScratchBytes + 2 * (size_t)ntiles * kRqTile);
+  const int64_t row = blockIdx.x;
+  uint4 a, b;
+  load_pencil(x + row * ldx, t * kRqTile + lane * 16, K, a, b);
+  const float amax = wave_max(rotate_tile<LOG4G>(a, b, t, K, lane, scratch, rowbuf));
+  if (lane == 0) maxes[t] = amax;
+  __syncthreads();
+  float m = 0.0f;
+  for (int i = 0; i < ntiles; ++i) m = fmaxf(m, maxes[i]);
+  const RowScale rs = row_scale<LOG4G>(m);
+  if (threadIdx.x == 0) s[row] = rs.sx;
+  quantize_tile(rowbuf, t, K, lane, rs, q + row * ldq);  // this wave's own tile: its writes are visible to it
 }
 
 template __global__ void rotate_quant_kernel<1>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
 template __global__ void rotate_quant_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
 template __global__ void rotate_quant_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
 template __global__ void rotate_quant_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
+template __global__ void rotate_quant_row_kernel<1>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
+template __global__ void rotate_quant_row_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
+template __global__ void rotate_quant_row_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
+template __global__ void rotate_quant_row_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
 
 }  // namespace hf

@@ -1,0 +1,111 @@
+// INT8 x INT8 -> INT32 partial products for at most 64 rows (timestep / text-conditioning modulation, short audio
+// streams): the accumulator of int8_mm_kernel (src/hyperflow_h3_flash/int8.py:302-306) for a K chunk, written as an
+// int32 plane that splitk_epilogue_kernel adds up and finishes.
+//
+// With M <= 64 the weight stream is all the traffic (N x K bytes against 64 x K of activations), so the work is cut
+// into many small weight slices: a work item is 128 weight rows x one K chunk (blockIdx.x = n tile, blockIdx.y =
+// chunk), enough items to give every CU several. A stage is 128 bytes of K for the 128 weight rows and the 64
+// activation rows (24 KiB), global -> LDS with buffer_load ... lds as whole 128-byte lines (8 lanes per row), in a
+// 3-stage ring (72 KiB, so two work items share a CU and one's start overlaps the other's tail): two stages in flight
+// while one is multiplied. Wave w multiplies weight rows 32w..32w+31 against all
+// 64 activation rows: v_mfma_i32_32x32x32_i8 with the weight as the first operand, two blocks per K step.
+#include "common.h"
+
+namespace hf {
+
+constexpr int kSkinnyM = 64;                          // activation rows (all of them)
+constexpr int kSkinnyN = 128;                         // weight rows per work item
+constexpr int kSkinnyStageK = 128;                    // K bytes per stage
+constexpr int kSkinnyWBytes = kSkinnyN * kSkinnyStageK;   // 16 KiB
+constexpr int kSkinnyStageBytes = kSkinnyWBytes + kSkinnyM * kSkinnyStageK;  // 24 KiB
+constexpr int kSkinnyStages = 3;
+constexpr int kSkinnyLds = kSkinnyStages * kSkinnyStageBytes;  // 72 KiB
+constexpr int kSkinnyLoads = 6;                       // per wave and stage: 4 weight blocks + 2 activation blocks
+
+__device__ __forceinline__ int skinny_swz(int r) { return (r & 7) ^ ((r >> 3) & 3); }
+
+__global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __restrict__ q, int64_t ldq,
+                                                             const int8_t* __restrict__ w, int64_t ldw,
+                                                             int32_t* __restrict__ acc, int64_t ld_acc,
+                                                             int64_t plane, int M, int N, int K, int k_chunk) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char sk_smem_raw[];
+  unsigned char HF_LDS* smem = (unsigned char HF_LDS*)sk_smem_raw;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane & 31, half = lane >> 5;
+  const int n0 = blockIdx.x * kSkinnyN;
+  const int k_lo = blockIdx.y * k_chunk;
+  const int k_len = min(K - k_lo, k_chunk);
+  const int rows_n = min(kSkinnyN, N - n0);
+  const uint32_t bytes_w = (uint32_t)(rows_n * ldw), bytes_q = (uint32_t)(M * ldq);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + (int64_t)n0 * ldw + k_lo, bytes_w - (uint32_t)k_lo);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + k_lo, bytes_q - (uint32_t)k_lo);
+
+  // Stage t -> slot t % 3. Every stage issues 6 loads per wave, stages past the chunk read zeros, so "stage t has
+  // landed" is always vmcnt(6) with the next stage in flight.
+  auto issue = [&](int t) {
+    unsigned char HF_LDS* st = smem + (t % kSkinnyStages) * kSkinnyStageBytes;
+    const int k0 = t * kSkinnyStageK;
+#pragma unroll
+    for (int i = 0; i < kSkinnyLoads; ++i) {
+      const bool isq = i >= 4;
+      const int blk = isq ? 2 * wave + (i - 4) : 4 * wave + i;
+      const int row = 8 * blk + (lane >> 3);
+      const int c = (lane & 7) ^ skinny_swz(row);
+      const int64_t ld = isq ? ldq : ldw;
+      const int rows_valid = isq ? M : rows_n;
+      const uint32_t oob = isq ? bytes_q : bytes_w;
+      const uint32_t voff = ((row < rows_valid) & (k0 + c * 16 < k_len)) ? (uint32_t)(row * ld + k0 + c * 16) : oob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(isq ? rq : rw,
+                                               (void HF_LDS*)(st + (isq ? kSkinnyWBytes : 0) + blk * 1024), 16, voff,
+                                               0, 0, 0);
+    }
+  };
+
+  v16i acc_r[2];
+  acc_r[0] = (v16i){0};
+  acc_r[1] = (v16i){0};
+  const int nst = (k_len + kSkinnyStageK - 1) / kSkinnyStageK;
+#pragma unroll
+  for (int t = 0; t < kSkinnyStages - 1; ++t) issue(t);
+  const int wrow = wave * 32 + sub;
+  for (int t = 0; t < nst; ++t) {
+    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(t + kSkinnyStages - 1);
+    const unsigned char HF_LDS* st = smem + (t % kSkinnyStages) * kSkinnyStageBytes;
+#pragma unroll
+    for (int ks = 0; ks < kSkinnyStageK / 32; ++ks) {
+      const int chunk = 2 * ks + half;
+      const v4i wf = *(const v4i HF_LDS*)(st + wrow * 128 + ((chunk ^ skinny_swz(wrow)) << 4));
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        const int qrow = jb * 32 + sub;
+        const v4i qf = *(const v4i HF_LDS*)(st + kSkinnyWBytes + qrow * 128 + ((chunk ^ skinny_swz(qrow)) << 4));
+        acc_r[jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, qf, acc_r[jb], 0, 0, 0);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // zero-fill loads past the chunk may still be landing
+
+  // Lane (sub, h) holds row m = 32jb + sub, columns n0 + 32w + 8g + 4h + (0..3) in registers 4g..4g+3.
+  int32_t* out = acc + blockIdx.y * plane;
+#pragma unroll
+  for (int jb = 0; jb < 2; ++jb) {
+    const int m = jb * 32 + sub;
+    if (m >= M) continue;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = n0 + wave * 32 + 8 * g + 4 * half;
+      int32_t* dst = out + (int64_t)m * ld_acc + n;
+      const v16i& c = acc_r[jb];
+      if (n + 4 <= N) {
+        *reinterpret_cast<v4i*>(dst) = (v4i){c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) dst[e] = c[4 * g + e];
+      }
+    }
+  }
+}
+
+}  // namespace hf

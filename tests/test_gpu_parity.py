@@ -105,6 +105,19 @@ def test_rotate_quant_groups_and_partial_tiles(oracle_lib, group, m, k):
     np.testing.assert_array_equal(q.cpu().numpy(), xq)
 
 
+@pytest.mark.parametrize("m,k", [(3, 14336), (3, 16384), (1025, 1024), (1024, 13824), (2, 77312)])
+def test_rotate_quant_both_row_layouts(oracle_lib, m, k):
+    """Up to 1024 rows of at most 14 tiles run one workgroup per row; more rows or wider rows run one wave per row.
+    Both against the oracle, on either side of each threshold and at the widest supported row."""
+    from hyperflow_h3_flash_amd.int8 import rotate_quant
+
+    inp = oracle_lib.make_inputs(m, k, 8, 256, outlier_frac=0.005, outlier_scale=30.0, seed=m + k)
+    q, s = rotate_quant(to_dev_bf16(inp["x"]), 256)
+    sx, xq = oracle_lib.quantize(oracle_lib.rotate(inp["x"], 256))
+    np.testing.assert_array_equal(s.cpu().numpy(), sx)
+    np.testing.assert_array_equal(q.cpu().numpy(), xq)
+
+
 def test_rotate_quant_zero_rows_wide_spans_and_strides(oracle_lib):
     from hyperflow_h3_flash_amd.int8 import rotate_quant
 
