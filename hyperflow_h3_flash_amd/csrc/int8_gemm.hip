@@ -115,6 +115,11 @@ __device__ __forceinline__ void tile_src(const GemmArgs& a, int id, TileSrc& t) 
   const bool live = id < tiles * a.splits;
   t.split = live ? id / tiles : 0;
   if (live) tile_of(id - t.split * tiles, a.tiles_m, a.tiles_n, tm, tn);
+  // The divisions above run on the vector unit; their results are uniform. Keeping them (and so the descriptors)
+  // in scalar registers avoids a per-load loop over lanes.
+  tm = __builtin_amdgcn_readfirstlane(tm);
+  tn = __builtin_amdgcn_readfirstlane(tn);
+  t.split = __builtin_amdgcn_readfirstlane(t.split);
   t.k_lo = t.split * a.k_chunk;
   t.k_hi = min(a.K, t.k_lo + a.k_chunk);
   t.m0 = tm * GBM;
@@ -366,15 +371,20 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       for (int j = 0; j < kStageLoads; ++j) load_one(a, nxt, ll, 0, j, slot_at(g + s), wv);
     });
     first_steps(s + 1);
-    kstep(f1, nothing, nothing);
-
-    // ------------------------------------------------------------------------------------------------ epilogue
-    // Every wave is done with the last stage's slot, the epilogue slot E: in low-rank mode it receives the tile's
-    // low-rank operands, which land while the accumulators are dequantized; then it stages the output.
+    // The last K step multiplies fragments already in registers, so once every wave's reads have returned the last
+    // stage's slot is free: it becomes the epilogue slot E. In low-rank mode E receives the tile's low-rank operands
+    // (issued between the last K step's MFMAs), which land while the accumulators are dequantized; then E stages
+    // the output.
     unsigned char HF_LDS* eslot = slot_at(g + nk - 1);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     HF_BARRIER();
-    if constexpr (kLr) load_lowrank(a, cur, eslot, wv, lane);
+    if constexpr (kLr) {
+      kstep(f1, nothing, [&] { load_lowrank(a, cur, eslot, wv, lane); });
+    } else {
+      kstep(f1, nothing, nothing);
+    }
+
+    // ------------------------------------------------------------------------------------------------ epilogue
 
     // Per-lane epilogue indices from an opaque copy of the lane id: keeps the compiler from hoisting their address
     // arithmetic out of the tile loop, where it would stay live (and spill) across the main loop.
@@ -437,29 +447,43 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
               c[i2][jb][v] = ((float)acc[ib][jb][v] * sxv[jb]) * params[256 + nl];
             }
         }
+        if constexpr (kLr) {
+          // Low-rank term: first operand up[n, :], second u[m, :], 16 ranks per MFMA, accumulated onto the
+          // dequantized values. The operands have landed once nothing is in flight; the barrier makes that true
+          // for every wave's loads. Rank steps outermost and unrolled: the 6 fragment reads of a step serve its 8
+          // independent MFMAs (the u fragments are shared by both column blocks), and the next step's reads are
+          // issued while they run. Always four steps, straight-line: ranks past r read as zero (load_lowrank), so
+          // they add exact zeros.
+          if (pb == 0) {
+            wait_vm(0);
+            HF_BARRIER();
+          }
+          auto lr_step = [&](int kk) {
+            const int chunk = 2 * kk + ehalf;
+            v8bf pf[2], uf[4];
+#pragma unroll
+            for (int i2 = 0; i2 < 2; ++i2) {
+              const int nl = wn * WN + (pb + i2) * 32 + esub;
+              pf[i2] = *(const v8bf HF_LDS*)(up_lds + nl * GBK + ((chunk ^ row_swz(nl)) << 4));
+            }
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+              const int ml = wm * 128 + jb * 32 + esub;
+              uf[jb] = *(const v8bf HF_LDS*)(u_lds + ml * GBK + ((chunk ^ row_swz(ml)) << 4));
+            }
+#pragma unroll
+            for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+              for (int jb = 0; jb < 4; ++jb)
+                c[i2][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf[i2], uf[jb], c[i2][jb], 0, 0, 0);
+          };
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) lr_step(kk);
+        }
 #pragma unroll
         for (int i2 = 0; i2 < 2; ++i2) {
           const int ib = pb + i2;
-          if constexpr (kLr) {
-            // Low-rank term: first operand up[n, :], second u[m, :], 16 ranks per MFMA, accumulated onto the
-            // dequantized values. The operands have landed once nothing is in flight; the barrier makes that true
-            // for every wave's loads.
-            if (pb == 0 && i2 == 0) {
-              wait_vm(0);
-              HF_BARRIER();
-            }
-            const int nl = wn * WN + ib * 32 + esub;
-            for (int kk = 0; kk < a.r; kk += 16) {
-              const int chunk = kk / 8 + ehalf;
-              const v8bf pf = *(const v8bf HF_LDS*)(up_lds + nl * GBK + ((chunk ^ row_swz(nl)) << 4));
-#pragma unroll
-              for (int jb = 0; jb < 4; ++jb) {
-                const int ml = wm * 128 + jb * 32 + esub;
-                const v8bf uf = *(const v8bf HF_LDS*)(u_lds + ml * GBK + ((chunk ^ row_swz(ml)) << 4));
-                c[i2][jb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c[i2][jb], 0, 0, 0);
-              }
-            }
-          } else if (a.r > 0) {
+          if (!kLr && a.r > 0) {
             // Ranks above 64: the same product from global memory.
             const int nrow = min(n0 + wn * WN + ib * 32 + esub, a.N - 1);
             for (int kk = 0; kk < a.r; kk += 16) {
