@@ -4,6 +4,7 @@ Importing the package does not touch the GPU or load the HIP library; the first 
 """
 
 from .int8 import (
+    ACTIVATIONS,
     INT8_GEMMS,
     KERNEL_OPTIONS,
     ROTATE_QUANTS,
@@ -18,6 +19,7 @@ from .lowrank import RANK_MULTIPLE, LowRankLinear, fuse_qkv, set_lowrank_rank_mu
 __version__ = "0.1.0"
 
 __all__ = [
+    "ACTIVATIONS",
     "INT8_GEMMS",
     "KERNEL_OPTIONS",
     "ROTATE_QUANTS",

@@ -50,6 +50,8 @@ SIGNATURES = {
     "hf_int8_linear_ws_bytes": ([_I64, _I64, _I64], ctypes.c_int64),
     "hf_int8_linear_ws": ([_P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P, _I64, _I64, _I64, _I64, _P,
                            _I64, _P], ctypes.c_int),
+    "hf_int8_linear_act_ws": ([_P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _I64, _I64,
+                               _I64, _P, _I64, _P], ctypes.c_int),
     "hf_lowrank_up": ([_P, _I64, _P, _I64, _I32, _P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
     "hf_int8_linear": ([_P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
                        ctypes.c_int),

@@ -5,6 +5,7 @@
 * `apply_quantization` — the ``config.json`` ``quantization`` block: ``{"method": "int8_convrot", "group": G,
   "linears": [dotted names]}`` (transformer.py:194-198), ValueError for another method, and ``keep_input`` on
   ``attn.to_q`` / ``attn.to_k`` so Q, K and V share one quantized input (transformer.py:199-203).
+* `fuse_activations` — fold a feed-forward's tanh-GELU module into its `Int8RotLinear` projection's epilogue.
 * `quantize_weight` — the checkpoint format ``qweight = round(W R / wscale)``, ``wscale = absmax_row(W R) / 127``,
   computed in float64 (tests/test_int8.py:31-36). An offline conversion step for bf16/fp32 weights, not part of the
   forward pass.
@@ -46,6 +47,29 @@ def replace_linear(model: nn.Module, name: str, make: type[nn.Module], *args: An
     else:
         setattr(owner, attr, replacement)
     return replacement
+
+
+def fuse_activations(model: nn.Module) -> list[str]:
+    """Fold every tanh-GELU activation module whose projection is an `Int8RotLinear` into that linear's GEMM epilogue:
+    a module with a ``proj`` attribute and ``approximate == "tanh"`` whose forward is ``gelu(proj(x))`` (the
+    feed-forward's first ``net`` entry, transformer.py:75-99) is replaced by its ``proj`` with
+    ``activation="gelu_tanh"``. Returns the replaced modules' names."""
+    found = []
+    for name, module in model.named_modules():
+        proj = getattr(module, "proj", None)
+        if (type(module).__name__ == "GELU" and getattr(module, "approximate", None) == "tanh"
+                and isinstance(proj, Int8RotLinear) and proj.activation is None):
+            found.append(name)
+    for name in found:
+        owner_name, _, attr = name.rpartition(".")
+        owner = model.get_submodule(owner_name) if owner_name else model
+        gelu = owner[int(attr)] if isinstance(owner, nn.ModuleList) else getattr(owner, attr)
+        gelu.proj.activation = "gelu_tanh"
+        if isinstance(owner, nn.ModuleList):
+            owner[int(attr)] = gelu.proj
+        else:
+            setattr(owner, attr, gelu.proj)
+    return found
 
 
 def apply_quantization(model: nn.Module, quantization: dict[str, Any] | None) -> list[str]:
@@ -197,5 +221,5 @@ def save_partition(model: nn.Module, folder: str, config: dict[str, Any], *, max
     return [os.path.join(folder, n) for n in names]
 
 
-__all__ = ["CONFIG_NAME", "METHOD", "apply_quantization", "load_partition", "load_quantized", "prepare_model",
-           "quantize_weight", "read_config", "replace_linear", "save_partition", "shard_files"]
+__all__ = ["CONFIG_NAME", "METHOD", "apply_quantization", "fuse_activations", "load_partition", "load_quantized",
+           "prepare_model", "quantize_weight", "read_config", "replace_linear", "save_partition", "shard_files"]

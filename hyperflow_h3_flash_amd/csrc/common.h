@@ -31,6 +31,29 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
 }
 
+// Output activations a GEMM epilogue can apply to the bf16-rounded linear output (the input of the reference's
+// activation module is the bf16 linear output, so the value is rounded once before the activation and once after).
+constexpr int kActNone = 0;
+constexpr int kActGeluTanh = 1;
+
+// tanh-approximate GELU in fp32, torch's `gelu(approximate="tanh")` formula: 0.5 x (1 + tanh(u)) with
+// u = sqrt(2/pi) (x + 0.044715 x^3). tanh(u) = 1 - 2 / (exp(2u) + 1) from the hardware exp2 and reciprocal
+// (absolute error of tanh ~1e-7, the rounding error of fp32 near 1); exp2 saturates to 0 or inf, giving -1 or 1.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  constexpr float kTwoBetaLog2e = 2.0f * 0.7978845608028654f * 1.4426950408889634f;  // 2 sqrt(2/pi) log2(e)
+  const float p = fmaf(0.044715f * x, x, 1.0f);                                       // 1 + 0.044715 x^2
+  const float e = __builtin_amdgcn_exp2f((x * p) * kTwoBetaLog2e);                    // exp(2u)
+  const float t = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);                 // tanh(u)
+  return (0.5f * x) * (1.0f + t);
+}
+
+// The activation of a packed bf16 pair, rounded back to a packed bf16 pair.
+template <int ACT>
+__device__ __forceinline__ uint32_t activate_bf16x2(uint32_t pair) {
+  if constexpr (ACT == kActGeluTanh) return pack_bf16x2(gelu_tanh(bf16_lo(pair)), gelu_tanh(bf16_hi(pair)));
+  return pair;
+}
+
 // Rounds an fp64 value to 8 significant bits (bf16 precision) with round-to-nearest-even, once, directly from the
 // fp64 bits: the kept bits end at bit 13 of the high word; bit 12 is the rounding bit and bits 11..0 of the high
 // word plus the whole low word are sticky. Adding 0xFFF + (lsb | sticky_low) carries into bit 13 exactly when RNE

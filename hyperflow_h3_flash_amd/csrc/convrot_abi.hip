@@ -39,6 +39,10 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16Lr>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16, hf::kActGeluTanh>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActGeluTanh>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<1>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<2>),
@@ -92,7 +96,7 @@ int device_cus() {
 // Workgroups for the persistent GEMM: one per CU, at most one per work item.
 int gemm_grid(int64_t items) { return (int)std::min<int64_t>(items, device_cus()); }
 
-int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream) {
+int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream, int act = hf::kActNone) {
   allow_large_lds();
   a.tiles_m = (a.M + hf::GBM - 1) / hf::GBM;
   a.tiles_n = (a.N + hf::GBN - 1) / hf::GBN;
@@ -107,9 +111,15 @@ int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream) {
   if (i32) {
     hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutI32>, grid, block, hf::kGemmLds, stream, a);
   } else if (a.r > 0 && a.r <= 64) {
-    hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16Lr>, grid, block, hf::kGemmLds, stream, a);
+    if (act == hf::kActGeluTanh)
+      hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActGeluTanh>), grid, block, hf::kGemmLds, stream, a);
+    else
+      hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16Lr>, grid, block, hf::kGemmLds, stream, a);
   } else {
-    hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16>, grid, block, hf::kGemmLds, stream, a);
+    if (act == hf::kActGeluTanh)
+      hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16, hf::kActGeluTanh>), grid, block, hf::kGemmLds, stream, a);
+    else
+      hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16>, grid, block, hf::kGemmLds, stream, a);
   }
   return launch_status();
 }
@@ -243,7 +253,8 @@ int64_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
 int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
                      const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r,
                      const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
-                     int64_t ws_bytes, hf_stream_t stream) {
+                     int64_t ws_bytes, hf_stream_t stream, int act = hf::kActNone) {
+  if (act != hf::kActNone && act != hf::kActGeluTanh) return HF_ERR_ARGUMENT;
   if (M == 0 || N == 0) return (M < 0 || N < 0) ? HF_ERR_ARGUMENT : HF_OK;
   int st = check_gemm_operands(q, ldq, w, ldw, M, N, K);
   if (st != HF_OK) return st;
@@ -280,7 +291,7 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
     const int vec = aligned(y, 8) && (ldy % 4) == 0;
     hipLaunchKernelGGL(hf::splitk_epilogue_kernel, dim3((unsigned)blocks), dim3(64), 0, s,
                        static_cast<const int32_t*>(ws), ld_acc, M * ld_acc, plan.splits, sx, sw, r > 0 ? u : nullptr,
-                       ldu, r > 0 ? up : nullptr, ld_up, r, bias, y, ldy, (int)M, (int)N, (int)tiles_n, vec);
+                       ldu, r > 0 ? up : nullptr, ld_up, r, bias, y, ldy, (int)M, (int)N, (int)tiles_n, vec, act);
     return launch_status();
   }
   hf::GemmArgs a{};
@@ -288,7 +299,7 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
   a.u = r > 0 ? u : nullptr; a.ldu = ldu; a.up = r > 0 ? up : nullptr; a.ldup = ld_up; a.r = r;
   a.bias = bias; a.out = y; a.ldo = ldy; a.M = (int)M; a.N = (int)N; a.K = (int)K;
   a.out_vec16 = aligned(y, 16) && (ldy % 8) == 0;
-  return launch_gemm(a, false, s);
+  return launch_gemm(a, false, s, act);
 }
 
 
@@ -389,6 +400,14 @@ int hf_int8_linear_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw
                       const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
                       int64_t ws_bytes, hf_stream_t stream) {
   return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, M, N, K, ws, ws_bytes, stream);
+}
+
+int hf_int8_linear_act_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx,
+                          const float* sw, const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up,
+                          int32_t r, const uint16_t* bias, int32_t activation, uint16_t* y, int64_t ldy, int64_t M,
+                          int64_t N, int64_t K, void* ws, int64_t ws_bytes, hf_stream_t stream) {
+  return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, M, N, K, ws, ws_bytes, stream,
+                          activation);
 }
 
 int64_t hf_lowrank_down_ws_bytes(int64_t M, int64_t K, int32_t r) {

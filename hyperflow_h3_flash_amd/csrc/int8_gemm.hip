@@ -6,7 +6,8 @@
 //   y[m, n]   = bf16((f32(acc) * sx[m]) * sw[n])              two separately rounded fp32 products (int8.py:179)
 // extended with the low-rank branch and a bias (the composition with LowRankLinear, transformer.py:57-58):
 //   y[m, n]   = bf16((f32(acc) * sx[m]) * sw[n] + sum_j u[m, j] * up[n, j] + bias[n])
-// With no low-rank branch and no bias the output is bitwise the reference's.
+// With no low-rank branch and no bias the output is bitwise the reference's. Optionally the bf16 output then goes
+// through an activation and is rounded again (ACT: the FFN up-projection's tanh-GELU, transformer.py:75-99).
 //
 // Tiling: 256 (m) x 256 (n) output tile per workgroup (one workgroup per CU, persistent), 8 waves (two per SIMD) in
 // a 2 (m) x 4 (n) grid, each a 128 x 64 sub-tile of 4 x 2 v_mfma_i32_32x32x32_i8 blocks (128 accumulator
@@ -21,11 +22,11 @@
 // double-buffered in registers (the LDS reads of one 32-byte K step overlap the MFMAs of the previous one).
 // Out-of-range rows and K beyond the end read as zero through the buffer descriptor's range check.
 //
-// The slot of a tile's second-to-last stage is the epilogue's: it receives the tile's low-rank operands (u rows m
-// and up rows n, rank <= 64, one 128-byte row each) while the last stage is multiplied, then stages the bf16 output
-// so each store instruction writes 8 whole 128-byte lines. Meanwhile the other slot already receives the next
-// tile's first stage, and the next tile's second stage is issued into the epilogue slot once the stores are out:
-// loads never stop at a tile boundary.
+// The slot of a tile's last stage is the epilogue's: once every wave has read its last fragments it receives the
+// tile's low-rank operands (u rows m and up rows n, rank <= 64, one 128-byte row each) while the last K step is
+// multiplied, then stages the bf16 output so each store instruction writes 8 whole 128-byte lines. Meanwhile the
+// other slot already receives the next tile's first stage, and the next tile's second stage is issued into the
+// epilogue slot once the stores are out: loads never stop at a tile boundary.
 #include <type_traits>
 
 #include "common.h"
@@ -231,7 +232,7 @@ constexpr int kOutI32 = 0, kOutBf16 = 1, kOutBf16Lr = 2;
 
 // Persistent kernel: one workgroup per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... Every wave issues the
 // same number of memory operations in the same order, so every wait is a constant vmcnt.
-template <int OUT>
+template <int OUT, int ACT = kActNone>
 __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[];
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)smem_raw;
@@ -514,8 +515,8 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
             uint32_t w4[4][2];
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
-              w4[gq][0] = pack_bf16x2(c[i2][jb][4 * gq], c[i2][jb][4 * gq + 1]);
-              w4[gq][1] = pack_bf16x2(c[i2][jb][4 * gq + 2], c[i2][jb][4 * gq + 3]);
+              w4[gq][0] = activate_bf16x2<ACT>(pack_bf16x2(c[i2][jb][4 * gq], c[i2][jb][4 * gq + 1]));
+              w4[gq][1] = activate_bf16x2<ACT>(pack_bf16x2(c[i2][jb][4 * gq + 2], c[i2][jb][4 * gq + 3]));
             }
 #pragma unroll
             for (int w = 0; w < 2; ++w) {
@@ -615,5 +616,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
 template __global__ void int8_gemm_kernel<kOutI32>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16Lr>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16, kActGeluTanh>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16Lr, kActGeluTanh>(GemmArgs);
 
 }  // namespace hf

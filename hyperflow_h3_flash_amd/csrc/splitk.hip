@@ -2,7 +2,8 @@
 // epilogue of int8_gemm_kernel,
 //   y[m, n] = bf16((f32(sum_s acc_s[m, n]) * sx[m]) * sw[n] + sum_j u[m, j] * up[n, j] + bias[n]).
 // Integer partial sums add exactly in any order, so with no low-rank branch and no bias the output is bitwise the
-// reference's (src/hyperflow_h3_flash/int8.py:179), as from the unsplit GEMM.
+// reference's (src/hyperflow_h3_flash/int8.py:179), as from the unsplit GEMM. `act` applies the same output activation
+// as the GEMM's epilogue (kActNone or kActGeluTanh).
 //
 // With few rows (M <= a few hundred) the unsplit GEMM has fewer 256 x 256 tiles than the chip has CUs; splitting K
 // gives every CU a share of the weight stream, at the cost of writing and re-reading M x N int32 per split.
@@ -25,7 +26,7 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
                                                              const uint16_t* __restrict__ up, int64_t ldup, int r,
                                                              const uint16_t* __restrict__ bias,
                                                              uint16_t* __restrict__ y, int64_t ldy, int M, int N,
-                                                             int tiles_n, int vec) {
+                                                             int tiles_n, int vec, int act) {
   const int lane = threadIdx.x;
   const int sub = lane & 31, half = lane >> 5;
   const int m0 = (blockIdx.x / tiles_n) * kSkTileM, n0 = (blockIdx.x % tiles_n) * kSkTileN;
@@ -77,12 +78,18 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
       v[e] = c[4 * gq + e];
       if (bias && n + e < N) v[e] = v[e] + __uint_as_float((uint32_t)bias[n + e] << 16);
     }
+    uint32_t p01 = pack_bf16x2(v[0], v[1]), p23 = pack_bf16x2(v[2], v[3]);
+    if (act == kActGeluTanh) {
+      p01 = activate_bf16x2<kActGeluTanh>(p01);
+      p23 = activate_bf16x2<kActGeluTanh>(p23);
+    }
     uint16_t* dst = y + (int64_t)m * ldy + n;
     if (vec && n + 4 <= N) {
-      *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      *reinterpret_cast<uint2*>(dst) = make_uint2(p01, p23);
     } else {
+      const uint16_t h[4] = {(uint16_t)p01, (uint16_t)(p01 >> 16), (uint16_t)p23, (uint16_t)(p23 >> 16)};
       for (int e = 0; e < 4; ++e)
-        if (n + e < N) dst[e] = (uint16_t)f32_to_bf16_rne(v[e]);
+        if (n + e < N) dst[e] = h[e];
     }
   }
 }

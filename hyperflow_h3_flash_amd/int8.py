@@ -102,14 +102,19 @@ class Int8RotLinear(nn.Module):
     leaves its quantized input for the next layer, which reuses it if it receives the exact same, unmodified tensor.
     Any other layer clears it, so nothing outlives the projections (int8.py:127-159).
 
-    ``rank`` and ``bias`` are this build's fused extension; with their defaults the module and its state dict are
-    exactly the reference's.
+    ``rank``, ``bias`` and ``activation`` are this build's fused extension; with their defaults the module and its
+    state dict are exactly the reference's. ``activation="gelu_tanh"`` applies torch's ``gelu(approximate="tanh")``
+    to the bf16 output inside the GEMM (a feed-forward up-projection and its activation module in one kernel,
+    transformer.py:75-99); it adds no state.
     """
 
     _last_input: ClassVar[dict[str, Any]] = {}
 
-    def __init__(self, in_features: int, out_features: int, group: int, *, rank: int = 0, bias: bool = False) -> None:
+    def __init__(self, in_features: int, out_features: int, group: int, *, rank: int = 0, bias: bool = False,
+                 activation: str | None = None) -> None:
         super().__init__()
+        _activation_code(activation)
+        self.activation = activation
         if in_features % group:
             raise ValueError(f"in_features {in_features} is not a multiple of the Hadamard group {group}")
         if rank < 0:
@@ -137,6 +142,8 @@ class Int8RotLinear(nn.Module):
             text += f", rank={self.rank}"
         if self.bias is not None:
             text += ", bias=True"
+        if self.activation is not None:
+            text += f", activation={self.activation}"
         return text
 
     def _quantize(self, x: Tensor, x2: Tensor, kernels: SimpleNamespace) -> tuple[Tensor, Tensor]:
@@ -163,9 +170,10 @@ class Int8RotLinear(nn.Module):
         xq, sx = self._quantize(x, x2, kernels)
         if self.rank:
             u = kernels.lowrank_down(x2, self.down.weight)
-            y = kernels.int8_matmul(xq, self.qweight, sx, self.wscale, u=u, up=self.up.weight, bias=self.bias)
+            y = kernels.int8_matmul(xq, self.qweight, sx, self.wscale, u=u, up=self.up.weight, bias=self.bias,
+                                    activation=self.activation)
         else:
-            y = kernels.int8_matmul(xq, self.qweight, sx, self.wscale, bias=self.bias)
+            y = kernels.int8_matmul(xq, self.qweight, sx, self.wscale, bias=self.bias, activation=self.activation)
         return y.reshape(*shape[:-1], self.out_features).to(x.dtype)
 
 
@@ -261,9 +269,23 @@ def _pad_rank(u: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
     return u.contiguous(), up.contiguous()
 
 
+#: Output activations the GEMM epilogue applies (the C ABI's HF_ACT_* codes).
+ACTIVATIONS = {None: 0, "gelu_tanh": 1}
+
+
+def _activation_code(activation: str | None) -> int:
+    if activation not in ACTIVATIONS:
+        raise ValueError(f"unsupported activation {activation!r}; expected one of {sorted(map(str, ACTIVATIONS))}")
+    return ACTIVATIONS[activation]
+
+
 def int8_matmul(a: Tensor, b: Tensor, sa: Tensor, sb: Tensor, *, u: Tensor | None = None, up: Tensor | None = None,
-                bias: Tensor | None = None) -> Tensor:
-    """``bf16((f32(a @ b^T) * sa) * sb [+ u @ up^T] [+ bias])`` for a int8 [M, K], b int8 [N, K] (int8.py:376-390)."""
+                bias: Tensor | None = None, activation: str | None = None) -> Tensor:
+    """``bf16((f32(a @ b^T) * sa) * sb [+ u @ up^T] [+ bias])`` for a int8 [M, K], b int8 [N, K] (int8.py:376-390).
+
+    ``activation="gelu_tanh"`` then applies torch's ``gelu(approximate="tanh")`` to that bf16 output in the same
+    kernel (rounded to bf16 again), the feed-forward up-projection's activation (transformer.py:75-99)."""
+    act = _activation_code(activation)
     M, K = a.shape
     N = b.shape[0]
     if b.shape[1] != K:
@@ -282,11 +304,11 @@ def int8_matmul(a: Tensor, b: Tensor, sa: Tensor, sb: Tensor, *, u: Tensor | Non
     lib = _native.library()
     with torch.cuda.device(a.device):
         ws, nbytes = _workspace(a.device, lib.hf_int8_linear_ws_bytes(M, N, K))
-        status = lib.hf_int8_linear_ws(
+        status = lib.hf_int8_linear_act_ws(
             _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(sa), _ptr(sb),
             _ptr(u), u.stride(0) if u is not None else 0, _ptr(up), up.stride(0) if up is not None else 0, r,
-            _ptr(bias), _ptr(c), c.stride(0), M, N, K, _ptr(ws), nbytes, _stream(a.device))
-    _check(status, "hf_int8_linear_ws")
+            _ptr(bias), act, _ptr(c), c.stride(0), M, N, K, _ptr(ws), nbytes, _stream(a.device))
+    _check(status, "hf_int8_linear_act_ws")
     return c
 
 
@@ -321,6 +343,7 @@ def _kernels() -> SimpleNamespace:
 
 
 __all__ = [
+    "ACTIVATIONS",
     "INT8_GEMMS",
     "KERNEL_OPTIONS",
     "ROTATE_QUANTS",

@@ -15,6 +15,7 @@
  *                        extended with the low-rank + bias epilogue of      transformer.py:57-58
  *   hf_lowrank_down   <- `LowRankLinear.down(x)` (bf16 nn.Linear)          transformer.py:57-58
  *   hf_lowrank_up     <- `LowRankLinear.up(u)` (bf16 nn.Linear)            transformer.py:57-58
+ *   hf_int8_linear_act_ws <- the FFN up-projection + its activation       transformer.py:75-99
  *   hf_int8_gemm_i32  <- the int32 accumulator of `int8_mm_kernel`         int8.py:302-306 (torch._int_mm, :362)
  *   hf_convrot_linear <- `Int8RotLinear.forward` device branch             int8.py:161-171
  */
@@ -111,6 +112,21 @@ int hf_int8_linear_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw
                       const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
                       int64_t ws_bytes, hf_stream_t stream);
 
+/*
+ * hf_int8_linear_ws followed by an output activation: the bf16 output y above goes through `activation` and is
+ * rounded to bf16 again, inside the GEMM's epilogue (no extra pass over y):
+ *   HF_ACT_NONE       y unchanged (this is hf_int8_linear_ws)
+ *   HF_ACT_GELU_TANH  y = bf16(gelu_tanh(y)), gelu_tanh(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in fp32
+ * Replaces the feed-forward's up-projection followed by its activation module (transformer.py:75-99, the FFN `net`
+ * run by ChunkedFeedForward; torch's `gelu(approximate="tanh")` on the bf16 linear output). Any other activation
+ * value is HF_ERR_ARGUMENT.
+ */
+#define HF_ACT_NONE 0
+#define HF_ACT_GELU_TANH 1
+int hf_int8_linear_act_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx,
+                          const float* sw, const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up,
+                          int32_t r, const uint16_t* bias, int32_t activation, uint16_t* y, int64_t ldy, int64_t M,
+                          int64_t N, int64_t K, void* ws, int64_t ws_bytes, hf_stream_t stream);
 /*
  * The int32 accumulator alone: acc = q @ w^T (for parity checks). acc: int32 [M, ldacc], 16-byte aligned.
  * Same operand rules as hf_int8_linear.

@@ -13,7 +13,9 @@ numpy closed forms the tests pin it with:
 * ``rotate`` / ``quantize`` / ``int8_gemm`` / ``epilogue`` — int8.py:176-179 step by step;
 * ``lowrank_down`` / ``fused_epilogue`` — LowRankLinear (src/hyperflow_h3_flash/transformer.py:57-58) and a bias;
 * ``composition`` — the reference's own composition ``Int8RotLinear(x) + LowRankLinear(x) + bias`` in bf16 tensor
-  arithmetic, which is what the fused extension is graded against.
+  arithmetic, which is what the fused extension is graded against;
+* ``gelu_tanh`` — the feed-forward's activation module on a bf16 tensor (torch's ``gelu(approximate="tanh")``,
+  applied to the up-projection output, transformer.py:75-99), in float64 and rounded once.
 
 Every array crossing into C is a contiguous numpy array; bf16 tensors are carried as ``uint16`` bit patterns.
 """
@@ -233,6 +235,22 @@ def composition(y_int8_bits, x_bits, down_bits=None, up_bits=None, bias_bits=Non
     if bias_bits is not None:
         y = bf16_to_f32(f32_to_bf16(y + bf16_to_f32(bias_bits)[None, :]))
     return f32_to_bf16(y)
+
+
+def gelu_tanh(y_bits: np.ndarray) -> np.ndarray:
+    """``bf16(0.5 y (1 + tanh(sqrt(2/pi) (y + 0.044715 y^3))))`` of a bf16 tensor: the activation the reference's
+    feed-forward applies to its bf16 up-projection output (transformer.py:75-99, torch's ``gelu(approximate="tanh")``).
+    Evaluated like torch's CPU kernel: the bf16 values widened to fp32, then ``x*x*x``, ``kBeta*(x + kKappa*x^3)``,
+    ``0.5*x*(1 + tanh(inner))`` in fp32 with tanh correctly rounded to fp32, then rounded to bf16 (only the last bit
+    of torch's fp32 tanh can differ)."""
+    x = bf16_to_f32(np.asarray(y_bits, dtype=np.uint16)).astype(np.float32)
+    k_beta = np.float32(np.sqrt(2.0) * (2.0 / np.sqrt(np.pi)) * 0.5)
+    k_kappa = np.float32(0.044715)
+    with np.errstate(over="ignore"):  # |x| near the bf16 maximum: x^3 is inf and tanh saturates, as in fp32
+        inner = k_beta * (x + k_kappa * (x * x * x))
+    t = np.tanh(inner.astype(np.float64)).astype(np.float32)  # tanh correctly rounded to fp32
+    g = np.float32(0.5) * x * (np.float32(1.0) + t)
+    return f32_to_bf16(g.astype(np.float32))
 
 
 # ------------------------------------------------------------------------------------------------ seeded inputs

@@ -73,5 +73,12 @@ def test_argument_checks_reject_before_launching(lib):
     assert lib.hf_lowrank_up(fake, 16, fake, 16, 12, null, fake, 64, 4, 64, null) == -3  # r % 8
     assert lib.hf_lowrank_up(odd, 16, fake, 16, 16, null, fake, 64, 4, 64, null) == -3  # u alignment
     assert lib.hf_lowrank_up(null, 16, null, 16, 16, null, null, 64, 0, 64, null) == 0  # no rows: no-op
+    # an activation code the epilogue does not know, even with nothing to compute
+    assert lib.hf_int8_linear_act_ws(fake, 128, fake, 128, fake, fake, null, 0, null, 0, 0, null, 7, fake, 64, 4, 64,
+                                     128, null, 0, null) == -1
+    assert lib.hf_int8_linear_act_ws(null, 128, null, 128, null, null, null, 0, null, 0, 0, null, 2, null, 64, 0, 64,
+                                     128, null, 0, null) == -1
+    assert lib.hf_int8_linear_act_ws(null, 128, null, 128, null, null, null, 0, null, 0, 0, null, 1, null, 64, 0, 64,
+                                     128, null, 0, null) == 0  # known activation, no rows: no-op
     # sizes beyond the kernels' index range
     assert lib.hf_int8_gemm_i32(fake, 1 << 24, fake, 128, fake, 64, 4, 64, 128, null) == -5

@@ -231,3 +231,30 @@ def test_fuse_qkv_checks_its_inputs():
         fuse_qkv(a, Int8RotLinear(64, 32, 16, rank=8))
     with pytest.raises(ValueError):
         fuse_qkv()
+
+
+class GELU(nn.Module):
+    """Stand-in with the attributes of a feed-forward's tanh-GELU projection module: `proj`, then the activation."""
+
+    def __init__(self, proj: nn.Module, approximate: str) -> None:
+        super().__init__()
+        self.proj, self.approximate = proj, approximate
+
+    def forward(self, x):
+        return nn.functional.gelu(self.proj(x), approximate=self.approximate)
+
+
+def test_fuse_activations_folds_tanh_gelu_into_the_int8_projection():
+    from hyperflow_h3_flash_amd.convert import fuse_activations
+
+    up = Int8RotLinear(64, 128, group=16)
+    ff = nn.Module()
+    ff.net = nn.ModuleList([GELU(up, "tanh"), nn.Dropout(0.0), Int8RotLinear(128, 64, group=16)])
+    ff.exact = GELU(Int8RotLinear(64, 128, group=16), "none")  # erf GELU: not the fused activation
+    ff.dense = GELU(nn.Linear(64, 128), "tanh")  # not an INT8 projection
+    names = fuse_activations(ff)
+    assert names == ["net.0"]
+    assert ff.net[0] is up and up.activation == "gelu_tanh"
+    assert isinstance(ff.exact, GELU) and isinstance(ff.dense, GELU)
+    assert ff.net[2].activation is None
+    assert fuse_activations(ff) == []  # idempotent

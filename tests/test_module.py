@@ -71,6 +71,16 @@ def test_extension_tensors_follow_lowrank_layout():
     assert "rank=8" in repr(layer) and "bias=True" in repr(layer)
 
 
+def test_activation_option_adds_no_state_and_is_checked():
+    plain = Int8RotLinear(64, 32, group=16, rank=8)
+    fused = Int8RotLinear(64, 32, group=16, rank=8, activation="gelu_tanh")
+    assert fused.state_dict().keys() == plain.state_dict().keys()
+    assert plain.activation is None and "activation" not in repr(plain)
+    assert "activation=gelu_tanh" in repr(fused)
+    with pytest.raises(ValueError, match="unsupported activation"):
+        Int8RotLinear(64, 32, group=16, activation="relu")
+
+
 def test_state_dict_round_trip_keeps_storage_dtypes():
     layer = Int8RotLinear(64, 32, group=16)
     with torch.no_grad():

@@ -299,3 +299,47 @@ def test_lowrank_up_planted_transpose_is_caught(oracle_lib):
     ref = oracle_lib.bf16_to_f32(f["lowrank"])[:, :32]
     assert (np.abs(right - ref) <= np.abs(ref) * 2.0**-7).all()
     assert not (np.abs(wrong - ref) <= np.abs(ref) * 2.0**-7).all()
+
+
+# ------------------------------------------------------------------------------------- feed-forward activation
+
+
+def test_gelu_tanh_matches_torch_on_every_bf16_value(oracle_lib):
+    """The oracle's activation against torch's own `gelu(approximate="tanh")` (the reference's activation module) on
+    every finite bf16 value: equal except where torch's fp32 tanh returns exactly -1 for an argument whose correctly
+    rounded tanh is the next float up (a few values near x = -5, outputs of order 1e-7 against 0)."""
+    import torch
+
+    bits = np.arange(65536, dtype=np.uint16)
+    bits = bits[np.isfinite(oracle_lib.bf16_to_f32(bits))]
+    ours = oracle_lib.gelu_tanh(bits)
+    x = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    theirs = torch.nn.functional.gelu(x, approximate="tanh").view(torch.int16).numpy().view(np.uint16)
+    diff = ours != theirs
+    assert diff.sum() <= 8
+    assert np.abs(oracle_lib.bf16_to_f32(ours[diff]) - oracle_lib.bf16_to_f32(theirs[diff])).max(initial=0) < 1e-6
+
+
+def test_gelu_tanh_closed_forms(oracle_lib):
+    """Special values fixed by the formula: gelu(0) = 0, gelu(x) -> x for large x and -> 0 for very negative x, and
+    gelu(1) = 0.5 (1 + tanh(sqrt(2/pi) * 1.044715)) = 0.8411920... (bf16 0.83984375)."""
+    x = oracle_lib.f32_to_bf16(np.array([0.0, 1.0, 30.0, -30.0, 3.0e38], dtype=np.float32))
+    g = oracle_lib.bf16_to_f32(oracle_lib.gelu_tanh(x))
+    assert g[0] == 0.0 and g[2] == 30.0 and g[3] == 0.0 and g[4] == oracle_lib.bf16_to_f32(x[4:5])[0]
+    exact = 0.5 * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * 1.044715))
+    assert g[1] == oracle_lib.bf16_to_f32(oracle_lib.f64_to_bf16(np.array([exact])))[0]
+
+
+def test_gelu_tanh_planted_mistake_is_caught(oracle_lib):
+    """A dropped cubic term (gelu with tanh(sqrt(2/pi) x)) fails the comparison with torch."""
+    import torch
+
+    rng = np.random.default_rng(3)
+    bits = oracle_lib.f32_to_bf16((rng.standard_normal(4096) * 3).astype(np.float32))
+    x = oracle_lib.bf16_to_f32(bits).astype(np.float64)
+    wrong = oracle_lib.f64_to_bf16(0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * x)))
+    theirs = torch.nn.functional.gelu(torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16),
+                                      approximate="tanh").view(torch.int16).numpy().view(np.uint16)
+    assert (wrong != theirs).sum() > 100
+    ours = oracle_lib.gelu_tanh(bits)
+    assert np.abs(oracle_lib.bf16_to_f32(ours) - oracle_lib.bf16_to_f32(theirs)).max() < 1e-6
