@@ -71,6 +71,24 @@ void allow_large_lds() {
   });
 }
 
+// rotate_quant_reg_kernel<lg, tpw> (both already range-checked by the caller).
+int launch_rotate_reg(int lg, int tpw, dim3 grid, dim3 block, size_t lds, hipStream_t s, const uint16_t* x,
+                      int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int K, int wpr) {
+#define HF_RQ_CASE(L, T)                                                                                          \
+  if (lg == L && tpw == T) {                                                                                      \
+    hipLaunchKernelGGL((hf::rotate_quant_reg_kernel<L, T>), grid, block, lds, s, x, ldx, q, ldq, sx, M, K, wpr);   \
+    return launch_status();                                                                                       \
+  }
+#define HF_RQ_CASES(L) HF_RQ_CASE(L, 1) HF_RQ_CASE(L, 2) HF_RQ_CASE(L, 3) HF_RQ_CASE(L, 4) HF_RQ_CASE(L, 5)
+  HF_RQ_CASES(1)
+  HF_RQ_CASES(2)
+  HF_RQ_CASES(3)
+  HF_RQ_CASES(4)
+#undef HF_RQ_CASES
+#undef HF_RQ_CASE
+  return HF_ERR_ARGUMENT;
+}
+
 int check_gemm_operands(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, int64_t M, int64_t N,
                         int64_t K) {
   if (!q || !w || M < 0 || N < 0 || K <= 0 || ldq < K || ldw < K) return HF_ERR_ARGUMENT;
@@ -347,6 +365,17 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
       default: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<4>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
     }
     return launch_status();
+  }
+  if (ntiles <= 4 * hf::kRqRegMaxTpw) {
+    // Rows held in registers: wpr waves of tpw tiles per row, 4 / wpr rows per workgroup.
+    const int wpr = (int)((ntiles + hf::kRqRegMaxTpw - 1) / hf::kRqRegMaxTpw);
+    const int tpw = (int)((ntiles + wpr - 1) / wpr);
+    const int rows_per_wg = std::max(1, 4 / wpr);
+    const int nw = wpr * rows_per_wg;
+    const int64_t blocks = (M + rows_per_wg - 1) / rows_per_wg;
+    if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+    return launch_rotate_reg(lg, tpw, dim3((unsigned)blocks), dim3(64 * nw), hf::rotate_quant_reg_lds_bytes(nw), s,
+                             x, ldx, q, ldq, sx, M, (int)K, wpr);
   }
   const size_t lds = hf::rotate_quant_lds_bytes(waves, (int)K);
   const int64_t blocks64 = (M + waves - 1) / waves;

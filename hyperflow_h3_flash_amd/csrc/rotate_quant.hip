@@ -53,13 +53,24 @@ __device__ __forceinline__ float quotient(float a, float d, float inv) {
 
 size_t rotate_quant_lds_bytes(int waves, int K) { return (size_t)waves * (kRqScratchBytes + 2 * (size_t)K); }
 
-// Rotates tile t of a row (elements 1024t .. 1024t + 1023; this lane's 16 consecutive inputs in cur0, cur1), rounds
-// every value once to bf16 and parks the bf16 bits in `rowbuf` (the row's buffer) at their natural positions.
-// Returns this lane's absmax of the rounded, still unnormalised sums. `scratch` is the wave's fp64 transpose area.
+// Element offset, within its 1024-element tile, of value 2i + h (h = 0, 1) of the 16 a lane holds after
+// rotate_tile_packed (the layout its last butterfly stage leaves):
+//   LOG4G <= 2: 16 lane + 2i + h                                   (natural order)
+//   LOG4G == 3: lane = 4 gi + cq: 64 gi + 16 (i / 2) + 4 cq + 2 (i % 2) + h
+//   LOG4G == 4: lane = 16 gi + b: 256 gi + 16 (2i + h) + b
 template <int LOG4G>
-__device__ __forceinline__ float rotate_tile(uint4 cur0, uint4 cur1, int t, int K, int lane, double* scratch,
-                                             uint16_t* rowbuf) {
-  const int e0 = t * kRqTile + lane * 16;
+__device__ __forceinline__ int held_offset(int lane, int i, int h) {
+  if constexpr (LOG4G <= 2) return 16 * lane + 2 * i + h;
+  if constexpr (LOG4G == 3) return 64 * (lane >> 2) + 16 * (i >> 1) + 4 * (lane & 3) + 2 * (i & 1) + h;
+  return 256 * (lane >> 4) + 16 * (2 * i + h) + (lane & 15);
+}
+
+// Rotates one 1024-element tile (this lane's 16 consecutive inputs 16 lane .. 16 lane + 15 in cur0, cur1), rounds
+// every value once to bf16 and returns them as 8 packed pairs (low half first) in the layout of held_offset, with
+// this lane's absmax of the rounded, still unnormalised sums. `scratch` is the wave's fp64 transpose area.
+template <int LOG4G>
+__device__ __forceinline__ float rotate_tile_packed(uint4 cur0, uint4 cur1, int lane, double* scratch,
+                                                    uint32_t (&packed)[8]) {
   float amax = 0.0f;
   double v[16];
   const uint32_t w[8] = {cur0.x, cur0.y, cur0.z, cur0.w, cur1.x, cur1.y, cur1.z, cur1.w};
@@ -70,23 +81,7 @@ __device__ __forceinline__ float rotate_tile(uint4 cur0, uint4 cur1, int t, int 
   }
   if constexpr (LOG4G >= 1) h4_stage<1>(v);
   if constexpr (LOG4G >= 2) h4_stage<4>(v);
-
-  if constexpr (LOG4G <= 2) {
-    // Values are in natural order: round, track the absmax, park 16 bf16 in the row buffer.
-    uint32_t packed[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float lo = round_f64_to_bf16_value(v[2 * i]);
-      float hi = round_f64_to_bf16_value(v[2 * i + 1]);
-      amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
-      packed[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
-    }
-    if (e0 < K) {
-      uint4* dst = reinterpret_cast<uint4*>(rowbuf + e0);
-      dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-      dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-    }
-  } else {
+  if constexpr (LOG4G >= 3) {
     // Transpose the fp64 pencils through LDS so each lane holds 16 values along digits 2 (and 3).
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -96,36 +91,59 @@ __device__ __forceinline__ float rotate_tile(uint4 cur0, uint4 cur1, int t, int 
       *reinterpret_cast<double2*>(scratch + lane * kRqStride + 2 * i) = pr;
     }
     wave_lds_sync();
-    int base_elem;
-    bool valid;
     if constexpr (LOG4G == 4) {
-      // lane = 16*gi + b; v[a] = pencil (16*gi + a), column b; element 256*gi + 16*a + b
+      // lane = 16*gi + b; v[a] = pencil (16*gi + a), column b
       const int gi = lane >> 4, b = lane & 15;
 #pragma unroll
       for (int a = 0; a < 16; ++a) v[a] = scratch[(16 * gi + a) * kRqStride + b];
-      base_elem = t * kRqTile + 256 * gi + b;
-      valid = t * kRqTile + 256 * gi < K;
       h4_stage<1>(v);
       h4_stage<4>(v);
     } else {
-      // lane = 4*gi + cq; v[4a + cc] = pencil (4*gi + a), column 4*cq + cc; element 64*gi + 16*a + 4*cq + cc
+      // lane = 4*gi + cq; v[4a + cc] = pencil (4*gi + a), column 4*cq + cc
       const int gi = lane >> 2, cq = lane & 3;
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) v[4 * a + cc] = scratch[(4 * gi + a) * kRqStride + 4 * cq + cc];
-      base_elem = t * kRqTile + 64 * gi + 4 * cq;
-      valid = t * kRqTile + 64 * gi < K;
       h4_stage<4>(v);
     }
     wave_lds_sync();  // scratch is rewritten by the next tile
+  }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float r = round_f64_to_bf16_value(v[i]);
-      amax = fmaxf(amax, fabsf(r));
-      if (valid) {
-        const int e = (LOG4G == 4) ? base_elem + 16 * i : base_elem + 16 * (i >> 2) + (i & 3);
-        rowbuf[e] = (uint16_t)(__float_as_uint(r) >> 16);
+  for (int i = 0; i < 8; ++i) {
+    const float lo = round_f64_to_bf16_value(v[2 * i]);
+    const float hi = round_f64_to_bf16_value(v[2 * i + 1]);
+    amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
+    packed[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+  }
+  return amax;
+}
+
+// Rotates tile t of a row and parks the rounded bf16 bits in `rowbuf` (the row's buffer) at their natural positions
+// (elements at or past K are not written). Returns this lane's absmax.
+template <int LOG4G>
+__device__ __forceinline__ float rotate_tile(uint4 cur0, uint4 cur1, int t, int K, int lane, double* scratch,
+                                             uint16_t* rowbuf) {
+  uint32_t packed[8];
+  const float amax = rotate_tile_packed<LOG4G>(cur0, cur1, lane, scratch, packed);
+  const int base = t * kRqTile;
+  if constexpr (LOG4G <= 2) {
+    if (base + lane * 16 < K) {
+      uint4* dst = reinterpret_cast<uint4*>(rowbuf + base + lane * 16);
+      dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+      dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    }
+  } else {
+    // A lane's 16 values lie in one Hadamard group, which is wholly inside or wholly past K.
+    if (base + held_offset<LOG4G>(lane, 0, 0) < K) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (LOG4G == 3) {
+          *reinterpret_cast<uint32_t*>(rowbuf + base + held_offset<LOG4G>(lane, i, 0)) = packed[i];
+        } else {
+          rowbuf[base + held_offset<LOG4G>(lane, i, 0)] = (uint16_t)packed[i];
+          rowbuf[base + held_offset<LOG4G>(lane, i, 1)] = (uint16_t)(packed[i] >> 16);
+        }
       }
     }
   }
@@ -147,15 +165,8 @@ __device__ __forceinline__ RowScale row_scale(float amax) {
   return r;
 }
 
-// Quantizes this lane's 16 elements of tile t from the row buffer (int8.py:178) and writes them (16 bytes).
-__device__ __forceinline__ void quantize_tile(const uint16_t* rowbuf, int t, int K, int lane, const RowScale& rs,
-                                              int8_t* qrow) {
-  const int e0 = t * kRqTile + lane * 16;
-  if (e0 >= K) return;
-  const uint4* src = reinterpret_cast<const uint4*>(rowbuf + e0);
-  const uint4 a = src[0], b = src[1];
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  uint32_t out[4];
+// Quantizes 8 packed bf16 pairs (int8.py:178): value v = 2i + h of the pairs becomes byte v % 4 of out[v / 4].
+__device__ __forceinline__ void quantize_packed(const uint32_t (&w)[8], const RowScale& rs, uint32_t (&out)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t word = 0;
@@ -170,6 +181,18 @@ __device__ __forceinline__ void quantize_tile(const uint16_t* rowbuf, int t, int
     }
     out[i] = word;
   }
+}
+
+// Quantizes this lane's 16 elements of tile t from the row buffer (int8.py:178) and writes them (16 bytes).
+__device__ __forceinline__ void quantize_tile(const uint16_t* rowbuf, int t, int K, int lane, const RowScale& rs,
+                                              int8_t* qrow) {
+  const int e0 = t * kRqTile + lane * 16;
+  if (e0 >= K) return;
+  const uint4* src = reinterpret_cast<const uint4*>(rowbuf + e0);
+  const uint4 a = src[0], b = src[1];
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t out[4];
+  quantize_packed(w, rs, out);
   *reinterpret_cast<uint4*>(qrow + e0) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
@@ -245,6 +268,100 @@ __global__ __launch_bounds__(1024) void rotate_quant_row_kernel(const uint16_t* 
   if (threadIdx.x == 0) s[row] = rs.sx;
   quantize_tile(rowbuf, t, K, lane, rs, q + row * ldq);  // this wave's own tile: its writes are visible to it
 }
+
+// Many rows, rows up to 20 tiles: the rounded row stays in registers instead of an LDS row buffer, so a workgroup
+// needs only the fp64 transpose areas and occupancy is set by registers (3 waves per SIMD at 5 tiles per wave). A
+// row is split over `wpr` waves of TPW <= 5 consecutive tiles each; a workgroup holds 4 / wpr rows (one when
+// wpr = 3). The waves of a
+// row combine their absmax through LDS, then each quantizes its own tiles; the bytes of a tile go back to natural
+// order through the (now free) transpose area so every lane stores 16 consecutive bytes. Same arithmetic as
+// rotate_quant_kernel.
+template <int LOG4G>
+__device__ __forceinline__ void store_quantized_tile(const uint32_t (&out)[4], int base, int K, int lane,
+                                                     unsigned char* stage, int8_t* qrow) {
+  if constexpr (LOG4G <= 2) {
+    if (base + lane * 16 < K)
+      *reinterpret_cast<uint4*>(qrow + base + lane * 16) = make_uint4(out[0], out[1], out[2], out[3]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t two = (out[j >> 1] >> (16 * (j & 1))) & 0xffffu;  // values 2j, 2j + 1
+      if constexpr (LOG4G == 3) {
+        *reinterpret_cast<uint16_t*>(stage + held_offset<LOG4G>(lane, j, 0)) = (uint16_t)two;
+      } else {
+        stage[held_offset<LOG4G>(lane, j, 0)] = (unsigned char)two;
+        stage[held_offset<LOG4G>(lane, j, 1)] = (unsigned char)(two >> 8);
+      }
+    }
+    wave_lds_sync();
+    if (base + lane * 16 < K)
+      *reinterpret_cast<uint4*>(qrow + base + lane * 16) = *reinterpret_cast<const uint4*>(stage + lane * 16);
+    wave_lds_sync();  // the next tile rewrites the staging bytes
+  }
+}
+
+size_t rotate_quant_reg_lds_bytes(int waves) { return (size_t)waves * kRqScratchBytes + 16; }
+
+template <int LOG4G, int TPW>
+__global__ __launch_bounds__(256) void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                               int8_t* __restrict__ q, int64_t ldq,
+                                                               float* __restrict__ s, int64_t M, int K, int wpr) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  double* scratch = reinterpret_cast<double*>(smem + (size_t)wave * kRqScratchBytes);
+  float* maxes = reinterpret_cast<float*>(smem + (size_t)nwaves * kRqScratchBytes);
+  const int64_t row = (int64_t)blockIdx.x * (nwaves / wpr) + wave / wpr;
+  const int part = wave % wpr;
+  const bool live = row < M;
+  const int kvalid = live ? K : 0;  // a row past the matrix reads zeros and stores nothing
+  const uint16_t* xrow = x + (live ? row : 0) * ldx;
+  const int t0 = part * TPW;
+
+  uint32_t held[TPW][8];
+  float amax = 0.0f;
+  uint4 nxt0, nxt1;
+  load_pencil(xrow, t0 * kRqTile + lane * 16, kvalid, nxt0, nxt1);
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const uint4 cur0 = nxt0, cur1 = nxt1;
+    if (i + 1 < TPW) load_pencil(xrow, (t0 + i + 1) * kRqTile + lane * 16, kvalid, nxt0, nxt1);
+    amax = fmaxf(amax, rotate_tile_packed<LOG4G>(cur0, cur1, lane, scratch, held[i]));
+  }
+  amax = wave_max(amax);
+  if (lane == 0) maxes[wave] = amax;
+  __syncthreads();
+  float m = 0.0f;
+  for (int w = 0; w < wpr; ++w) m = fmaxf(m, maxes[(wave / wpr) * wpr + w]);
+  if (!live) return;
+  const RowScale rs = row_scale<LOG4G>(m);
+  if (part == 0 && lane == 0) s[row] = rs.sx;
+  int8_t* qrow = q + row * ldq;
+  unsigned char* stage = reinterpret_cast<unsigned char*>(scratch);  // the transpose area is free from here on
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int base = (t0 + i) * kRqTile;
+    if (base < K) {
+      uint32_t out[4];
+      quantize_packed(held[i], rs, out);
+      store_quantized_tile<LOG4G>(out, base, K, lane, stage, qrow);
+    }
+  }
+}
+
+constexpr int kRqRegMaxTpw = 5;  // tiles per wave (more registers would cut occupancy below 3 waves per SIMD)
+
+#define HF_RQ_REG(L, T)                                                                                            \
+  template __global__ void rotate_quant_reg_kernel<L, T>(const uint16_t*, int64_t, int8_t*, int64_t, float*,       \
+                                                         int64_t, int, int);
+#define HF_RQ_REG_ALL(L) HF_RQ_REG(L, 1) HF_RQ_REG(L, 2) HF_RQ_REG(L, 3) HF_RQ_REG(L, 4) HF_RQ_REG(L, 5)
+HF_RQ_REG_ALL(1)
+HF_RQ_REG_ALL(2)
+HF_RQ_REG_ALL(3)
+HF_RQ_REG_ALL(4)
+#undef HF_RQ_REG_ALL
+#undef HF_RQ_REG
 
 template __global__ void rotate_quant_kernel<1>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
 template __global__ void rotate_quant_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);

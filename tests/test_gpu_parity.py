@@ -105,15 +105,30 @@ def test_rotate_quant_groups_and_partial_tiles(oracle_lib, group, m, k):
     np.testing.assert_array_equal(q.cpu().numpy(), xq)
 
 
-@pytest.mark.parametrize("m,k", [(3, 14336), (3, 16384), (1025, 1024), (1024, 13824), (2, 77312)])
+@pytest.mark.parametrize("m,k", [(3, 14336), (3, 16384), (1025, 1024), (1024, 13824), (2, 77312), (1030, 5120),
+                                 (1100, 5376), (1027, 13824), (1025, 20480), (1025, 21504)])
 def test_rotate_quant_both_row_layouts(oracle_lib, m, k):
-    """Up to 1024 rows of at most 14 tiles run one workgroup per row; more rows or wider rows run one wave per row.
-    Both against the oracle, on either side of each threshold and at the widest supported row."""
+    """Up to 1024 rows of at most 14 tiles run one workgroup per row. More rows of up to 20 tiles keep the row in
+    registers, split over 1 (<= 5 tiles), 2 (6: a partial last tile), 3 (14) or 4 (20) waves per row; wider rows
+    run one wave per row with an LDS row buffer. All against the oracle, on either side of each threshold and at the
+    widest supported row."""
     from hyperflow_h3_flash_amd.int8 import rotate_quant
 
     inp = oracle_lib.make_inputs(m, k, 8, 256, outlier_frac=0.005, outlier_scale=30.0, seed=m + k)
     q, s = rotate_quant(to_dev_bf16(inp["x"]), 256)
     sx, xq = oracle_lib.quantize(oracle_lib.rotate(inp["x"], 256))
+    np.testing.assert_array_equal(s.cpu().numpy(), sx)
+    np.testing.assert_array_equal(q.cpu().numpy(), xq)
+
+
+@pytest.mark.parametrize("group", [4, 16, 64, 256])
+def test_rotate_quant_many_rows_every_group(oracle_lib, group):
+    """The register-resident layout for each butterfly depth (natural order up to G = 16, transposed for 64, 256)."""
+    from hyperflow_h3_flash_amd.int8 import rotate_quant
+
+    inp = oracle_lib.make_inputs(1031, 3072, 8, group, outlier_frac=0.01, outlier_scale=20.0, seed=group)
+    q, s = rotate_quant(to_dev_bf16(inp["x"]), group)
+    sx, xq = oracle_lib.quantize(oracle_lib.rotate(inp["x"], group))
     np.testing.assert_array_equal(s.cpu().numpy(), sx)
     np.testing.assert_array_equal(q.cpu().numpy(), xq)
 
