@@ -23,6 +23,7 @@ namespace hf {
 constexpr int kRqTile = 1024;                            // elements per wave step (64 lanes x 16)
 constexpr int kRqStride = 18;                            // doubles per pencil in the transpose scratch (16 + pad)
 constexpr int kRqScratchBytes = 64 * kRqStride * 8;      // 9216 bytes per wave
+constexpr int kRqRegMaxTpw = 5;  // tiles per wave of the register-resident kernel (held in at most 128 VGPRs)
 
 __device__ __forceinline__ void h4(double& a, double& b, double& c, double& d) {
   double s = (a + b) + (c + d);
@@ -302,10 +303,11 @@ __device__ __forceinline__ void store_quantized_tile(const uint32_t (&out)[4], i
 
 size_t rotate_quant_reg_lds_bytes(int waves) { return (size_t)waves * kRqScratchBytes + 16; }
 
+// Five tiles per wave fit 128 VGPRs (four waves per SIMD) when the compiler is held to it.
 template <int LOG4G, int TPW>
-__global__ __launch_bounds__(256) void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                               int8_t* __restrict__ q, int64_t ldq,
-                                                               float* __restrict__ s, int64_t M, int K, int wpr) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TPW == kRqRegMaxTpw ? 4 : 1)))
+void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
+                             float* __restrict__ s, int64_t M, int K, int wpr) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -319,15 +321,22 @@ __global__ __launch_bounds__(256) void rotate_quant_reg_kernel(const uint16_t* _
   const uint16_t* xrow = x + (live ? row : 0) * ldx;
   const int t0 = part * TPW;
 
+  // held[i] first receives tile i's raw pencil (all of this wave's loads in flight at once), then its rounded
+  // values.
   uint32_t held[TPW][8];
-  float amax = 0.0f;
-  uint4 nxt0, nxt1;
-  load_pencil(xrow, t0 * kRqTile + lane * 16, kvalid, nxt0, nxt1);
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
-    const uint4 cur0 = nxt0, cur1 = nxt1;
-    if (i + 1 < TPW) load_pencil(xrow, (t0 + i + 1) * kRqTile + lane * 16, kvalid, nxt0, nxt1);
-    amax = fmaxf(amax, rotate_tile_packed<LOG4G>(cur0, cur1, lane, scratch, held[i]));
+    uint4 a, b;
+    load_pencil(xrow, (t0 + i) * kRqTile + lane * 16, kvalid, a, b);
+    held[i][0] = a.x; held[i][1] = a.y; held[i][2] = a.z; held[i][3] = a.w;
+    held[i][4] = b.x; held[i][5] = b.y; held[i][6] = b.z; held[i][7] = b.w;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const uint4 a = make_uint4(held[i][0], held[i][1], held[i][2], held[i][3]);
+    const uint4 b = make_uint4(held[i][4], held[i][5], held[i][6], held[i][7]);
+    amax = fmaxf(amax, rotate_tile_packed<LOG4G>(a, b, lane, scratch, held[i]));
   }
   amax = wave_max(amax);
   if (lane == 0) maxes[wave] = amax;
@@ -349,8 +358,6 @@ __global__ __launch_bounds__(256) void rotate_quant_reg_kernel(const uint16_t* _
     }
   }
 }
-
-constexpr int kRqRegMaxTpw = 5;  // tiles per wave (more registers would cut occupancy below 3 waves per SIMD)
 
 #define HF_RQ_REG(L, T)                                                                                            \
   template __global__ void rotate_quant_reg_kernel<L, T>(const uint16_t*, int64_t, int8_t*, int64_t, float*,       \
