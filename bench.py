@@ -54,7 +54,33 @@ def parse_args():
                    help="workload: 2 (default) is the headline QKV projection; 1, 3, 4, 5 are supporting measurements")
     p.add_argument("--copy-probe", action="store_true",
                    help="only copy a 1 GiB device buffer 3 times (calibrates the HBM byte counters) and exit")
+    p.add_argument("--vendor-gemm", action="store_true",
+                   help="only time the vendor library's own INT8, FP8 and bf16 GEMMs at the headline shape (a "
+                        "calibration of what the matrix cores sustain, not this build's path) and exit")
     return p.parse_args()
+
+
+def vendor_gemm(torch, steps, warmup):
+    """hipBLASLt (through torch) at M=32768 N=15360 K=5120: INT8 -> INT32, FP8 e4m3fn -> bf16, bf16 -> bf16."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    m, n, k = M, N, K
+    cases = {}
+    a8 = torch.randint(-127, 128, (m, k), device=dev, generator=gen, dtype=torch.int8)
+    b8 = torch.randint(-127, 128, (n, k), device=dev, generator=gen, dtype=torch.int8)
+    cases["int8_int_mm"] = lambda: torch._int_mm(a8, b8.t())
+    af = torch.randn(m, k, device=dev, generator=gen).to(torch.float8_e4m3fn)
+    bf = torch.randn(n, k, device=dev, generator=gen).to(torch.float8_e4m3fn)
+    one = torch.ones((), device=dev)
+    cases["fp8_e4m3fn_scaled_mm"] = lambda: torch._scaled_mm(af, bf.t(), scale_a=one, scale_b=one,
+                                                             out_dtype=torch.bfloat16)
+    ab = torch.randn(m, k, device=dev, generator=gen, dtype=torch.bfloat16)
+    bb = torch.randn(n, k, device=dev, generator=gen, dtype=torch.bfloat16)
+    cases["bf16_matmul"] = lambda: ab @ bb.t()
+    for name, fn in cases.items():
+        t = timed(torch, fn, steps, warmup)
+        print(json.dumps({"vendor_gemm": name, "M": m, "N": n, "K": k, "us": round(t * 1e6, 1),
+                          "tera_ops": round(2.0 * m * n * k / t / 1e12, 1)}), flush=True)
 
 
 def copy_probe(torch):
@@ -131,6 +157,9 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.vendor_gemm:
+        vendor_gemm(torch, args.steps, args.warmup)
+        return
     if args.copy_probe:
         copy_probe(torch)
         return
