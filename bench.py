@@ -19,6 +19,9 @@ parity-test shapes and supporting measurements, not the headline line):
   5  small M in {64, 256, 1024}, K=5120, N in {5120, 30720}, rank 32: HBM GB/s over the compulsory bytes, with
      enough weight copies rotated per step that the weights come from HBM, not the 256 MiB Infinity Cache; the
      layer calls are captured in a HIP graph and replayed (the per-call host work would otherwise dominate)
+  6  the model's gated FFN on M=32768: up 5376->28672 (14336 hidden + 14336 gate rows), SwiGLU in bf16, down
+     14336->5376, rank 64; timed unfused (torch chunk + silu + multiply between the layers) and fused (SwiGLU in
+     the up-projection's GEMM epilogue)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--config N]
 """
@@ -50,8 +53,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=32768, help="row sample for the CPU baseline")
-    p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
-                   help="workload: 2 (default) is the headline QKV projection; 1, 3, 4, 5 are supporting measurements")
+    p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6),
+                   help="workload: 2 (default) is the headline QKV projection; 1, 3-6 are supporting measurements")
     p.add_argument("--copy-probe", action="store_true",
                    help="only copy a 1 GiB device buffer 3 times (calibrates the HBM byte counters) and exit")
     p.add_argument("--vendor-gemm", action="store_true",
@@ -319,9 +322,11 @@ def run_config(torch, config, steps, warmup):
                    hbm_GBs=round(linear_bytes(m, k, n, r, True) / t / 1e9, 1),
                    config={"workload": "single convrot linear", "M": m, "K": k, "N": n, "group": GROUP,
                            "rank": r, "bias": True})
-    elif config in (3, 4):
+    elif config in (3, 4, 6):
         if config == 3:
             m, shapes, name = 32768, [(5120, 13824), (13824, 5120)], "FFN up + tanh-GELU + down"
+        elif config == 6:
+            m, shapes, name = 32768, [(5376, 28672), (14336, 5376)], "gated FFN up + SwiGLU + down"
         else:
             m = 41344
             shapes, name = [(5120, 15360), (5120, 5120), (5120, 13824), (13824, 5120)], "DiT block linears"
@@ -332,8 +337,8 @@ def run_config(torch, config, steps, warmup):
 
         def step():
             with torch.no_grad():
-                if config == 3:
-                    # The up-projection applies the tanh-GELU in its GEMM epilogue (activation="gelu_tanh").
+                if config in (3, 6):
+                    # The up-projection applies the activation in its GEMM epilogue (layers[0].activation).
                     layers[1](layers[0](xs[0]))
                 else:
                     for x, layer in zip(xs, layers):
@@ -342,12 +347,16 @@ def run_config(torch, config, steps, warmup):
         def step_unfused():
             with torch.no_grad():
                 h = layers[0](xs[0])
-                layers[1](torch.nn.functional.gelu(h, approximate="tanh"))
+                if config == 3:
+                    layers[1](torch.nn.functional.gelu(h, approximate="tanh"))
+                else:
+                    hidden, gate = h.chunk(2, dim=-1)
+                    layers[1](hidden * torch.nn.functional.silu(gate))
 
         extra = {}
-        if config == 3:
+        if config in (3, 6):
             t_unfused = timed(torch, step_unfused, steps, warmup)
-            layers[0].activation = "gelu_tanh"
+            layers[0].activation = "gelu_tanh" if config == 3 else "swiglu"
             extra = {"unfused_ms_per_step": round(t_unfused * 1e3, 4)}
         t = timed(torch, step, steps, warmup)
         ops = sum(2.0 * m * n * k for k, n in shapes)
@@ -355,7 +364,8 @@ def run_config(torch, config, steps, warmup):
                    ms_per_step=round(t * 1e3, 4), higher_is_better=True,
                    pct_of_peak=round(100.0 * ops / t / 1e12 / PEAK_INT8_TOPS, 2), **extra,
                    config={"workload": name, "M": m, "shapes_KN": shapes, "group": GROUP, "rank": 64,
-                           "bias": False, "activation": "fused tanh-GELU epilogue" if config == 3 else None})
+                           "bias": False,
+                           "activation": {3: "fused tanh-GELU epilogue", 6: "fused SwiGLU epilogue"}.get(config)})
     else:
         k = 5120
         for m in (64, 256, 1024):

@@ -5,7 +5,8 @@
 * `apply_quantization` — the ``config.json`` ``quantization`` block: ``{"method": "int8_convrot", "group": G,
   "linears": [dotted names]}`` (transformer.py:194-198), ValueError for another method, and ``keep_input`` on
   ``attn.to_q`` / ``attn.to_k`` so Q, K and V share one quantized input (transformer.py:199-203).
-* `fuse_activations` — fold a feed-forward's tanh-GELU module into its `Int8RotLinear` projection's epilogue.
+* `fuse_activations` — fold a feed-forward's tanh-GELU or SwiGLU module into its `Int8RotLinear` projection's
+  epilogue.
 * `quantize_weight` — the checkpoint format ``qweight = round(W R / wscale)``, ``wscale = absmax_row(W R) / 127``,
   computed in float64 (tests/test_int8.py:31-36). An offline conversion step for bf16/fp32 weights, not part of the
   forward pass.
@@ -50,26 +51,34 @@ def replace_linear(model: nn.Module, name: str, make: type[nn.Module], *args: An
 
 
 def fuse_activations(model: nn.Module) -> list[str]:
-    """Fold every tanh-GELU activation module whose projection is an `Int8RotLinear` into that linear's GEMM epilogue:
-    a module with a ``proj`` attribute and ``approximate == "tanh"`` whose forward is ``gelu(proj(x))`` (the
-    feed-forward's first ``net`` entry, transformer.py:75-99) is replaced by its ``proj`` with
-    ``activation="gelu_tanh"``. Returns the replaced modules' names."""
+    """Fold every feed-forward activation module whose projection is an `Int8RotLinear` into that linear's GEMM
+    epilogue (the feed-forward's first ``net`` entry, transformer.py:75-99), replacing the module by its ``proj``:
+
+    * a ``GELU`` module with ``approximate == "tanh"`` (forward ``gelu(proj(x))``) -> ``activation="gelu_tanh"``;
+    * a ``SwiGLU`` module (forward ``h, g = proj(x).chunk(2, -1); h * silu(g)``, the model's gated feed-forward)
+      -> ``activation="swiglu"``, when its projection's width is a multiple of 32.
+
+    Returns the replaced modules' names."""
     found = []
     for name, module in model.named_modules():
         proj = getattr(module, "proj", None)
-        if (type(module).__name__ == "GELU" and getattr(module, "approximate", None) == "tanh"
-                and isinstance(proj, Int8RotLinear) and proj.activation is None):
-            found.append(name)
-    for name in found:
+        if not isinstance(proj, Int8RotLinear) or proj.activation is not None:
+            continue
+        kind = type(module).__name__
+        if kind == "GELU" and getattr(module, "approximate", None) == "tanh":
+            found.append((name, "gelu_tanh"))
+        elif kind == "SwiGLU" and proj.out_features % 32 == 0:
+            found.append((name, "swiglu"))
+    for name, activation in found:
         owner_name, _, attr = name.rpartition(".")
         owner = model.get_submodule(owner_name) if owner_name else model
-        gelu = owner[int(attr)] if isinstance(owner, nn.ModuleList) else getattr(owner, attr)
-        gelu.proj.activation = "gelu_tanh"
+        act = owner[int(attr)] if isinstance(owner, nn.ModuleList) else getattr(owner, attr)
+        act.proj.activation = activation
         if isinstance(owner, nn.ModuleList):
-            owner[int(attr)] = gelu.proj
+            owner[int(attr)] = act.proj
         else:
-            setattr(owner, attr, gelu.proj)
-    return found
+            setattr(owner, attr, act.proj)
+    return [name for name, _ in found]
 
 
 def apply_quantization(model: nn.Module, quantization: dict[str, Any] | None) -> list[str]:

@@ -35,6 +35,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // activation module is the bf16 linear output, so the value is rounded once before the activation and once after).
 constexpr int kActNone = 0;
 constexpr int kActGeluTanh = 1;
+constexpr int kActSwiGLU = 2;  // the output is hidden * silu(gate) of column pairs (see glu_row)
 
 // tanh-approximate GELU in fp32, torch's `gelu(approximate="tanh")` formula: 0.5 x (1 + tanh(u)) with
 // u = sqrt(2/pi) (x + 0.044715 x^3). tanh(u) = 1 - 2 / (exp(2u) + 1) from the hardware exp2 and reciprocal
@@ -45,6 +46,41 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   const float e = __builtin_amdgcn_exp2f((x * p) * kTwoBetaLog2e);                    // exp(2u)
   const float t = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);                 // tanh(u)
   return (0.5f * x) * (1.0f + t);
+}
+
+// Gated-linear-unit weights (2F rows: F "hidden" rows and F "gate" rows, the feed-forward's SwiGLU projection) are
+// multiplied in pair order: GEMM column n uses weight row glu_row(n). Within each 32 columns come 16 hidden rows and
+// then the 16 gate rows of the same outputs, so in the 32x32 MFMA layout one lane holds both columns of an output
+// (registers v and v + 8, v < 8). gate_first: the weight's first F rows are the gates.
+__device__ __forceinline__ int glu_row(int n, int half_n, int gate_first) {
+  return ((n >> 5) << 4) + (n & 15) + ((((n >> 4) & 1) ^ gate_first) ? half_n : 0);
+}
+
+// fp32 -> the nearest bf16 value (round to nearest even), as a float.
+__device__ __forceinline__ float round_bf16(float x) { return bf16_lo(pack_bf16x2(x, x)); }
+
+// SiLU in fp32, torch's formula x / (1 + exp(-x)). exp(-x) comes from the hardware exp2 (inf below x = -88.7, as
+// fp32 exp overflows there, giving -0). The quotient is the hardware reciprocal's product refined by one residual
+// step, q - (q d - x) / d (Markstein's correction; this sign arrangement keeps silu(-0) = -0), which rounds as the
+// IEEE division does in all but rare cases: the bare product is off by one fp32 ulp often enough to move bf16
+// roundings. The reciprocal of d > 2^100 is taken of d 2^-100 and the quotient scaled back (exact powers of two),
+// so values of 1 / d below the normal range are not flushed to zero.
+__device__ __forceinline__ float silu(float x) {
+  const float e = __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
+  const float d = 1.0f + e;
+  const bool big = e > 0x1p100f;
+  const float ds = big ? d * 0x1p-100f : d;
+  const float r = __builtin_amdgcn_rcpf(ds);
+  float q = x * r;
+  const float refined = fmaf(-fmaf(q, ds, -x), r, q);
+  q = __builtin_fabsf(q) < __builtin_inff() ? refined : q;  // x = inf: the residual is NaN, the product is the value
+  q = big ? q * 0x1p-100f : q;
+  return e == __builtin_inff() ? x * 0.0f : q;
+}
+
+// The reference's SwiGLU on bf16 tensors: bf16(h * bf16(silu(g))) of the bf16 linear outputs h and g.
+__device__ __forceinline__ float swiglu(float h_bf16, float g_bf16) {
+  return round_bf16(h_bf16 * round_bf16(silu(g_bf16)));
 }
 
 // The activation of a packed bf16 pair, rounded back to a packed bf16 pair.

@@ -43,6 +43,10 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActGeluTanh>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16, hf::kActSwiGLU>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActSwiGLU>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<1>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<2>),
@@ -131,11 +135,15 @@ int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream, int act = hf::kAc
   } else if (a.r > 0 && a.r <= 64) {
     if (act == hf::kActGeluTanh)
       hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActGeluTanh>), grid, block, hf::kGemmLds, stream, a);
+    else if (act == hf::kActSwiGLU)
+      hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActSwiGLU>), grid, block, hf::kGemmLds, stream, a);
     else
       hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16Lr>, grid, block, hf::kGemmLds, stream, a);
   } else {
     if (act == hf::kActGeluTanh)
       hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16, hf::kActGeluTanh>), grid, block, hf::kGemmLds, stream, a);
+    else if (act == hf::kActSwiGLU)
+      hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16, hf::kActSwiGLU>), grid, block, hf::kGemmLds, stream, a);
     else
       hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16>, grid, block, hf::kGemmLds, stream, a);
   }
@@ -271,18 +279,26 @@ int64_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
 int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
                      const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r,
                      const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
-                     int64_t ws_bytes, hf_stream_t stream, int act = hf::kActNone) {
-  if (act != hf::kActNone && act != hf::kActGeluTanh) return HF_ERR_ARGUMENT;
+                     int64_t ws_bytes, hf_stream_t stream, int act_code = HF_ACT_NONE) {
+  if (act_code < HF_ACT_NONE || act_code > HF_ACT_SWIGLU_GATE_FIRST) return HF_ERR_ARGUMENT;
+  const bool glu = act_code == HF_ACT_SWIGLU || act_code == HF_ACT_SWIGLU_GATE_FIRST;
+  const int act = glu ? hf::kActSwiGLU : (act_code == HF_ACT_GELU_TANH ? hf::kActGeluTanh : hf::kActNone);
+  // SwiGLU: the N weight rows are F hidden and F gate rows (F = N / 2 output columns), F a multiple of 16.
+  if (glu && (N < 0 || N % 32)) return HF_ERR_ARGUMENT;
+  const int64_t n_out = glu ? N / 2 : N;
   if (M == 0 || N == 0) return (M < 0 || N < 0) ? HF_ERR_ARGUMENT : HF_OK;
   int st = check_gemm_operands(q, ldq, w, ldw, M, N, K);
   if (st != HF_OK) return st;
-  if (!sx || !sw || !y || ldy < N || r < 0) return HF_ERR_ARGUMENT;
+  if (!sx || !sw || !y || ldy < n_out || r < 0) return HF_ERR_ARGUMENT;
   if (!aligned(y, 8)) return HF_ERR_ALIGNMENT;
   if (r > 0) {
     if (!u || !up || ldu < r || ld_up < r) return HF_ERR_ARGUMENT;
     if ((r % 8) || !aligned(u, 16) || !aligned(up, 16) || (ldu % 8) || (ld_up % 8)) return HF_ERR_ALIGNMENT;
     if (512 * ldu >= (int64_t(1) << 31) || 512 * ld_up >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   }
+  // Pair order reads the weight (and up) through one buffer descriptor each: 32-bit byte offsets.
+  if (glu && (N * ldw >= (int64_t(1) << 32) || (r > 0 && N * ld_up * 2 >= (int64_t(1) << 32)))) return HF_ERR_SIZE;
+  const int glu_half = (int)(N / 2), glu_gate_first = act_code == HF_ACT_SWIGLU_GATE_FIRST;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const GemmPlan plan = gemm_plan(M, N, K);
   const int64_t ld_acc = (N + 3) / 4 * 4;
@@ -309,7 +325,8 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
     const int vec = aligned(y, 8) && (ldy % 4) == 0;
     hipLaunchKernelGGL(hf::splitk_epilogue_kernel, dim3((unsigned)blocks), dim3(64), 0, s,
                        static_cast<const int32_t*>(ws), ld_acc, M * ld_acc, plan.splits, sx, sw, r > 0 ? u : nullptr,
-                       ldu, r > 0 ? up : nullptr, ld_up, r, bias, y, ldy, (int)M, (int)N, (int)tiles_n, vec, act);
+                       ldu, r > 0 ? up : nullptr, ld_up, r, bias, y, ldy, (int)M, (int)N, (int)tiles_n, vec, act,
+                       glu_half, glu_gate_first);
     return launch_status();
   }
   hf::GemmArgs a{};
@@ -317,6 +334,7 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
   a.u = r > 0 ? u : nullptr; a.ldu = ldu; a.up = r > 0 ? up : nullptr; a.ldup = ld_up; a.r = r;
   a.bias = bias; a.out = y; a.ldo = ldy; a.M = (int)M; a.N = (int)N; a.K = (int)K;
   a.out_vec16 = aligned(y, 16) && (ldy % 8) == 0;
+  a.glu_half = glu_half; a.glu_gate_first = glu_gate_first;
   return launch_gemm(a, false, s, act);
 }
 

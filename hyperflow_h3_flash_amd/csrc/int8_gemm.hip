@@ -77,6 +77,10 @@ struct GemmArgs {
   int splits;            // 1: no split
   int k_chunk;           // multiple of GBK
   int64_t split_stride;
+  // Gated-linear-unit pair order (the ACT == kActSwiGLU kernels): column n multiplies weight row
+  // glu_row(n, glu_half, glu_gate_first), the per-column wscale, bias and up rows follow it, and the output has
+  // N / 2 columns.
+  int glu_half, glu_gate_first;
 };
 
 // Workgroup id -> (tile_m, tile_n). The dispatcher deals workgroup ids round robin to the 8 XCDs (XCD = id % 8,
@@ -110,6 +114,7 @@ struct TileSrc {
   __amdgpu_buffer_rsrc_t rq, rw;
 };
 
+template <bool GLU>
 __device__ __forceinline__ void tile_src(const GemmArgs& a, int id, TileSrc& t) {
   int tm = 0, tn = 0;
   const int tiles = a.tiles_m * a.tiles_n;
@@ -128,9 +133,22 @@ __device__ __forceinline__ void tile_src(const GemmArgs& a, int id, TileSrc& t) 
   t.rows_m = live ? min(GBM, a.M - t.m0) : 0;
   t.rows_n = live ? min(GBN, a.N - t.n0) : 0;
   t.bytes_q = (uint32_t)(t.rows_m * a.ldq);
-  t.bytes_w = (uint32_t)(t.rows_n * a.ldw);
   t.rq = make_rsrc(a.q + (int64_t)t.m0 * a.ldq, t.bytes_q);
-  t.rw = make_rsrc(a.w + (int64_t)t.n0 * a.ldw, t.bytes_w);
+  if (GLU) {
+    // Pair order scatters the tile's columns over both halves of the weight: one descriptor for all of it.
+    t.bytes_w = (uint32_t)((int64_t)a.N * a.ldw);
+    t.rw = make_rsrc(a.w, t.bytes_w);
+  } else {
+    t.bytes_w = (uint32_t)(t.rows_n * a.ldw);
+    t.rw = make_rsrc(a.w + (int64_t)t.n0 * a.ldw, t.bytes_w);
+  }
+}
+
+// The weight row of tile column `col` (0..255) relative to the tile's descriptor: the column itself, or in pair
+// order its global row. Eight consecutive columns starting at a multiple of 8 map to eight consecutive rows.
+template <bool GLU>
+__device__ __forceinline__ int weight_row(const GemmArgs& a, const TileSrc& t, int col) {
+  return GLU ? glu_row(t.n0 + col, a.glu_half, a.glu_gate_first) : col;
 }
 
 // The per-lane part of a stage load's address, the same for every tile. Load i of a wave fills the 1 KiB block
@@ -145,6 +163,7 @@ struct LaneLoad {
 // Load j of this wave's share of stage kt, into slot `slot`: j < kBlkPerWave fills q block kBlkPerWave * wave + j,
 // the others w block kBlkPerWave * wave + j - kBlkPerWave. Rows past the tile's valid rows and chunks at or past K read as zero (the offset moves
 // past the descriptor), branch-free; so does every load of a stage past the end.
+template <bool GLU>
 __device__ __forceinline__ void load_one(const GemmArgs& a, const TileSrc& t, const LaneLoad& ll, int kt, int j,
                                          unsigned char HF_LDS* slot, int wave) {
   const int i = j % kBlkPerWave;
@@ -156,7 +175,8 @@ __device__ __forceinline__ void load_one(const GemmArgs& a, const TileSrc& t, co
   const int row = row0 + ll.lrow;
   const uint32_t cb = ll.chunk ^ (uint32_t)(16 * (i & 3));
   const uint32_t k0 = (uint32_t)(t.k_lo + kt * GBK);
-  const uint32_t off = (isw ? ll.row_w : ll.row_q) + (uint32_t)(row0 * ld) + cb + k0;
+  const int src_row0 = isw ? weight_row<GLU>(a, t, row0) : row0;
+  const uint32_t off = (isw ? ll.row_w : ll.row_q) + (uint32_t)(src_row0 * ld) + cb + k0;
   const uint32_t voff = ((row < rows_valid) & (k0 + cb < (uint32_t)t.k_hi)) ? off : oob;  // '&': no branch
   __builtin_amdgcn_raw_ptr_buffer_load_lds(isw ? t.rw : t.rq,
                                            (void HF_LDS*)(slot + (isw ? kAStage : 0) + (row0 / 8) * 1024), 16,
@@ -166,6 +186,7 @@ __device__ __forceinline__ void load_one(const GemmArgs& a, const TileSrc& t, co
 // The low-rank operands of a tile (u rows m into the slot's q half, up rows n into its w half, rank r <= 64: one
 // 128-byte row each; chunks past r and rows past the tile's valid rows read as zero), in as many loads per wave as
 // a stage.
+template <bool GLU>
 __device__ __forceinline__ void load_lowrank(const GemmArgs& a, const TileSrc& t, unsigned char HF_LDS* slot,
                                              int wave, int lane) {
 #pragma unroll
@@ -173,12 +194,15 @@ __device__ __forceinline__ void load_lowrank(const GemmArgs& a, const TileSrc& t
     const bool isup = j >= kBlkPerWave;
     const int64_t ld_bytes = (isup ? a.ldup : a.ldu) * 2;
     const int rows_valid = isup ? t.rows_n : t.rows_m;
-    const uint32_t bytes = (uint32_t)(rows_valid * ld_bytes);
+    const bool whole = isup && GLU;  // pair order: up rows follow the weight rows, anywhere in up
+    const uint32_t bytes = (uint32_t)((whole ? a.N : rows_valid) * ld_bytes);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(
-        isup ? (const void*)(a.up + (int64_t)t.n0 * a.ldup) : (const void*)(a.u + (int64_t)t.m0 * a.ldu), bytes);
+        isup ? (const void*)(a.up + (whole ? 0 : (int64_t)t.n0 * a.ldup)) : (const void*)(a.u + (int64_t)t.m0 * a.ldu),
+        bytes);
     const int blk = kBlkPerWave * wave + j % kBlkPerWave, r = 8 * blk + (lane >> 3);
+    const int src_r = (isup ? weight_row<GLU>(a, t, 8 * blk) : 8 * blk) + (lane >> 3);
     const int c = (lane & 7) ^ row_swz(r);
-    const uint32_t voff = ((r < rows_valid) & (c * 8 < a.r)) ? (uint32_t)(r * ld_bytes + c * 16) : bytes;
+    const uint32_t voff = ((r < rows_valid) & (c * 8 < a.r)) ? (uint32_t)(src_r * ld_bytes + c * 16) : bytes;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (void HF_LDS*)(slot + (isup ? kAStage : 0) + blk * 1024), 16,
                                              voff, 0, 0, 0);
   }
@@ -241,9 +265,10 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   const int wm = wave & 1, wn = wave >> 1;  // 2 (m) x (kWaves / 2) (n) waves of 128 x WN
   const int sub = lane & 31, half = lane >> 5;
   constexpr bool kLr = OUT == kOutBf16Lr;
+  constexpr bool kGlu = ACT == kActSwiGLU;  // pair order (the glu fields of GemmArgs)
   // Stores per wave of a full tile, when the wait for the next stage 0 behind them fits the 6-bit wait counter
   // (else they are drained).
-  constexpr int kTileStores = GBM * GBN * (OUT == kOutI32 ? 4 : 2) / (kWaves * 1024);
+  constexpr int kTileStores = GBM * GBN * (OUT == kOutI32 ? 4 : 2) / (ACT == kActSwiGLU ? 2 : 1) / (kWaves * 1024);
   constexpr int kFastStores = kTileStores + kStageLoads <= 63 ? kTileStores : 0;
   float HF_LDS* params = (float HF_LDS*)(smem + kRingBytes);
   const int pt = threadIdx.x & 255;
@@ -264,11 +289,11 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   ll.row_w = (uint32_t)((lane >> 3) * a.ldw);
   ll.chunk = (uint32_t)(((lane & 7) ^ (lane >> 3)) << 4);
   TileSrc cur;
-  tile_src(a, id, cur);
+  tile_src<kGlu>(a, id, cur);
 #pragma unroll
-  for (int j = 0; j < kStageLoads; ++j) load_one(a, cur, ll, 0, j, slot_at(0), wave);
+  for (int j = 0; j < kStageLoads; ++j) load_one<kGlu>(a, cur, ll, 0, j, slot_at(0), wave);
 #pragma unroll
-  for (int j = 0; j < kStageLoads; ++j) load_one(a, cur, ll, 1, j, slot_at(1), wave);
+  for (int j = 0; j < kStageLoads; ++j) load_one<kGlu>(a, cur, ll, 1, j, slot_at(1), wave);
 
   int g = 0;  // slot parity of the current tile's stage 0
   Frags f0, f1;
@@ -316,7 +341,9 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     float p_val = 0.0f, p_ws = 0.0f;
     uint32_t p_bias = 0;
     if (OUT != kOutI32) {
-      const int mr = min(cur.m0 + pt, a.M - 1), nc = min(cur.n0 + pt, a.N - 1);
+      const int mr = min(cur.m0 + pt, a.M - 1);
+      const int ncol = min(cur.n0 + pt, a.N - 1);
+      const int nc = kGlu ? glu_row(ncol, a.glu_half, a.glu_gate_first) : ncol;
       const uint16_t* bsrc = a.bias ? a.bias : reinterpret_cast<const uint16_t*>(a.sw);
       if (kThreads == 256 || threadIdx.x < 256) {
         p_val = a.sx[mr];
@@ -359,17 +386,17 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       first_steps(s);
       boundary(s, [&] {
 #pragma unroll
-        for (int j = 0; j < kStageLoads; ++j) load_one(a, cur, ll, s + 2, j, slot_at(g + s), wv);
+        for (int j = 0; j < kStageLoads; ++j) load_one<kGlu>(a, cur, ll, s + 2, j, slot_at(g + s), wv);
       });
     }
     // Stage nk - 2 refills its slot with the next tile's stage 0; stage nk - 1 has no successor.
     const int next_id = id + gridDim.x;
     TileSrc nxt;
-    tile_src(a, next_id, nxt);
+    tile_src<kGlu>(a, next_id, nxt);
     first_steps(s);
     boundary(s, [&] {
 #pragma unroll
-      for (int j = 0; j < kStageLoads; ++j) load_one(a, nxt, ll, 0, j, slot_at(g + s), wv);
+      for (int j = 0; j < kStageLoads; ++j) load_one<kGlu>(a, nxt, ll, 0, j, slot_at(g + s), wv);
     });
     first_steps(s + 1);
     // The last K step multiplies fragments already in registers, so once every wave's reads have returned the last
@@ -380,7 +407,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     HF_BARRIER();
     if constexpr (kLr) {
-      kstep(f1, nothing, [&] { load_lowrank(a, cur, eslot, wv, lane); });
+      kstep(f1, nothing, [&] { load_lowrank<kGlu>(a, cur, eslot, wv, lane); });
     } else {
       kstep(f1, nothing, nothing);
     }
@@ -431,6 +458,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       // Packed bf16 results, two 16-byte chunks per block: pk[ib][jb][0..3] is chunk 4ib + 2h, pk[ib][jb][4..7]
       // chunk 4ib + 2h + 1 of row esub of block (ib, jb), h = ehalf.
       uint32_t pk[NB][4][8];
+      uint32_t gk[NB][4][4];  // pair order: the 16 outputs of a block, 8 per lane half
       const bool has_bias = a.bias != nullptr;
       // Two column blocks at a time (the fp32 values of two blocks are 128 registers): dequantize, add the low-rank
       // term, the bias, convert.
@@ -486,7 +514,8 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
           const int ib = pb + i2;
           if (!kLr && a.r > 0) {
             // Ranks above 64: the same product from global memory.
-            const int nrow = min(n0 + wn * WN + ib * 32 + esub, a.N - 1);
+            const int ncol = min(n0 + wn * WN + ib * 32 + esub, a.N - 1);
+            const int nrow = kGlu ? glu_row(ncol, a.glu_half, a.glu_gate_first) : ncol;
             for (int kk = 0; kk < a.r; kk += 16) {
               const int k = kk + 8 * ehalf;
               const v8bf pf =
@@ -509,6 +538,26 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
 #pragma unroll
               for (int v = 0; v < 16; ++v)
                 c[i2][jb][v] = c[i2][jb][v] + params[512 + wn * WN + ib * 32 + 8 * (v >> 2) + 4 * ehalf + (v & 3)];
+          }
+          if constexpr (ACT == kActSwiGLU) {
+            // Pair order: register v < 8 is the hidden column and v + 8 the gate column of output
+            // 8 (v / 4) + 4 h + v % 4 of the block's 16. After one exchange between the lane halves, lane (sub, h)
+            // holds outputs 8h .. 8h + 7 of row sub: gk[ib][jb][0..3].
+#pragma unroll
+            for (int jb = 0; jb < 4; ++jb) {
+              uint32_t w[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                w[i] = pack_bf16x2(swiglu(round_bf16(c[i2][jb][2 * i]), round_bf16(c[i2][jb][2 * i + 8])),
+                                   swiglu(round_bf16(c[i2][jb][2 * i + 1]), round_bf16(c[i2][jb][2 * i + 9])));
+              const auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+              const auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+              gk[ib][jb][0] = s02[0];
+              gk[ib][jb][1] = s13[0];
+              gk[ib][jb][2] = s02[1];
+              gk[ib][jb][3] = s13[1];
+            }
+            continue;
           }
 #pragma unroll
           for (int jb = 0; jb < 4; ++jb) {
@@ -547,6 +596,39 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       }
       unsigned char HF_LDS* stage_out = eslot + wave * 8192;
       uint16_t* out = static_cast<uint16_t*>(a.out);
+      if constexpr (ACT == kActSwiGLU) {
+        // Pair order: the wave's outputs are 128 rows x 16 NB columns (64-byte rows, swizzle64) in one round; each
+        // store instruction writes 16 rows x 64 bytes, and the four waves of a row band fill whole lines together.
+        static_assert(NB == 2, "pair order is laid out for 8 waves");
+        const int n_out = a.N / 2, no0 = n0 / 2 + wn * (WN / 2);
+#pragma unroll
+        for (int ib = 0; ib < NB; ++ib)
+#pragma unroll
+          for (int jb = 0; jb < 4; ++jb) {
+            const int row = jb * 32 + esub;
+            *(v4i HF_LDS*)(stage_out + row * 64 + (swizzle64(row, 2 * ib + ehalf) << 4)) =
+                (v4i){(int)gk[ib][jb][0], (int)gk[ib][jb][1], (int)gk[ib][jb][2], (int)gk[ib][jb][3]};
+          }
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int row = 16 * i + (el >> 2), ch = el & 3;
+          const v4i val = *(const v4i HF_LDS*)(stage_out + row * 64 + (swizzle64(row, ch) << 4));
+          const int m = m0 + wm * 128 + row;
+          const int n = no0 + 8 * ch;
+          uint16_t* dst = out + (int64_t)m * a.ldo + n;
+          if (full) {
+            *reinterpret_cast<v4i*>(dst) = val;
+          } else if (m < a.M) {
+            if (a.out_vec16 && n + 8 <= n_out) {
+              *reinterpret_cast<v4i*>(dst) = val;
+            } else {
+              for (int e = 0; e < 8; ++e)
+                if (n + e < n_out) dst[e] = (uint16_t)((uint32_t)val[e >> 1] >> (16 * (e & 1)));
+            }
+          }
+        }
+      } else {
 #pragma unroll
       for (int pb = 0; pb < NB; pb += 2) {
 #pragma unroll
@@ -587,6 +669,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
           wave_lds_sync();  // the next round rewrites this wave's staging area
         }
       }
+      }
     }
     // A partial tile's guarded stores (and the r > 64 global reads) are not a fixed count, and too many stores do
     // not fit the wait counter next to the next tile's loads: drain everything.
@@ -598,7 +681,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     HF_BARRIER();
 #pragma unroll
-    for (int j = 0; j < kStageLoads; ++j) load_one(a, nxt, ll, 1, j, eslot, wv);
+    for (int j = 0; j < kStageLoads; ++j) load_one<kGlu>(a, nxt, ll, 1, j, eslot, wv);
     g += nk - 2;
     id = next_id;
     cur = nxt;
@@ -618,5 +701,7 @@ template __global__ void int8_gemm_kernel<kOutBf16>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16Lr>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16, kActGeluTanh>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16Lr, kActGeluTanh>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16, kActSwiGLU>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16Lr, kActSwiGLU>(GemmArgs);
 
 }  // namespace hf

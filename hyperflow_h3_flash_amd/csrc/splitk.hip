@@ -3,7 +3,11 @@
 //   y[m, n] = bf16((f32(sum_s acc_s[m, n]) * sx[m]) * sw[n] + sum_j u[m, j] * up[n, j] + bias[n]).
 // Integer partial sums add exactly in any order, so with no low-rank branch and no bias the output is bitwise the
 // reference's (src/hyperflow_h3_flash/int8.py:179), as from the unsplit GEMM. `act` applies the same output activation
-// as the GEMM's epilogue (kActNone or kActGeluTanh).
+// as the GEMM's epilogue (kActNone, kActGeluTanh, or kActSwiGLU).
+//
+// kActSwiGLU: the partials hold the N columns in the weight's natural order; the epilogue walks them in pair order
+// (logical column n reads accumulator column, wscale, bias and up row glu_row(n)), so in each 32-column tile register
+// v < 8 holds a hidden column and v + 8 its gate column, and the tile writes 16 of the N / 2 outputs.
 //
 // With few rows (M <= a few hundred) the unsplit GEMM has fewer 256 x 256 tiles than the chip has CUs; splitting K
 // gives every CU a share of the weight stream, at the cost of writing and re-reading M x N int32 per split.
@@ -26,7 +30,11 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
                                                              const uint16_t* __restrict__ up, int64_t ldup, int r,
                                                              const uint16_t* __restrict__ bias,
                                                              uint16_t* __restrict__ y, int64_t ldy, int M, int N,
-                                                             int tiles_n, int vec, int act) {
+                                                             int tiles_n, int vec, int act, int glu_half,
+                                                             int glu_gate_first) {
+  const bool glu = act == kActSwiGLU;
+  // Accumulator column of logical column n; four consecutive columns from a multiple of 4 stay consecutive.
+  auto col = [&](int n) { return glu ? glu_row(n, glu_half, glu_gate_first) : n; };
   const int lane = threadIdx.x;
   const int sub = lane & 31, half = lane >> 5;
   const int m0 = (blockIdx.x / tiles_n) * kSkTileM, n0 = (blockIdx.x % tiles_n) * kSkTileN;
@@ -36,6 +44,7 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
 #pragma unroll
   for (int gq = 0; gq < 4; ++gq) {
     const int n = n0 + 8 * gq + 4 * half;
+    const int na = (n < N) ? col(n) : n;
     int32_t s4[4] = {0, 0, 0, 0};
     if (m < M) {
       if (vec && n + 4 <= N) {
@@ -43,7 +52,7 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
         v4i pl[kSkMaxSplits];
 #pragma unroll
         for (int s = 0; s < kSkMaxSplits; ++s)
-          pl[s] = s < splits ? *reinterpret_cast<const v4i*>(acc + s * plane + (int64_t)m * ld_acc + n) : (v4i){0};
+          pl[s] = s < splits ? *reinterpret_cast<const v4i*>(acc + s * plane + (int64_t)m * ld_acc + na) : (v4i){0};
 #pragma unroll
         for (int s = 0; s < kSkMaxSplits; ++s)
 #pragma unroll
@@ -51,17 +60,17 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
       } else {
         for (int s = 0; s < splits; ++s)
           for (int e = 0; e < 4; ++e)
-            if (n + e < N) s4[e] += acc[s * plane + (int64_t)m * ld_acc + n + e];
+            if (n + e < N) s4[e] += acc[s * plane + (int64_t)m * ld_acc + na + e];
       }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float wsn = (n + e < N) ? sw[n + e] : 0.0f;
+      const float wsn = (n + e < N) ? sw[na + e] : 0.0f;
       c[4 * gq + e] = ((float)s4[e] * sxm) * wsn;
     }
   }
   // Low-rank term, 16 ranks per MFMA: first operand up[n, :], second u[m, :] (rows past the matrix read zero).
-  const int nrow = n0 + sub;
+  const int nrow = (n0 + sub < N) ? col(n0 + sub) : N;
   for (int kk = 0; kk < r; kk += 16) {
     const int k = kk + 8 * half;
     const v8bf pf = (k < r && nrow < N) ? *reinterpret_cast<const v8bf*>(up + (int64_t)nrow * ldup + k) : (v8bf){0};
@@ -69,15 +78,43 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c, 0, 0, 0);
   }
   if (m >= M) return;
+  if (bias) {
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int n = n0 + 8 * gq + 4 * half;
+      const int na = (n < N) ? col(n) : n;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) c[4 * gq + e] = c[4 * gq + e] + __uint_as_float((uint32_t)bias[na + e] << 16);
+    }
+  }
+  if (glu) {
+    // Outputs n0 / 2 + 8 gq + 4 h + e from the pair (v, v + 8), v = 4 gq + e.
+    const int n_out = N / 2;
+#pragma unroll
+    for (int gq = 0; gq < 2; ++gq) {
+      const int o = n0 / 2 + 8 * gq + 4 * half;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = swiglu(round_bf16(c[4 * gq + e]), round_bf16(c[4 * gq + 8 + e]));
+      const uint32_t p01 = pack_bf16x2(v[0], v[1]), p23 = pack_bf16x2(v[2], v[3]);
+      uint16_t* dst = y + (int64_t)m * ldy + o;
+      if (vec && o + 4 <= n_out) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(p01, p23);
+      } else {
+        const uint16_t h[4] = {(uint16_t)p01, (uint16_t)(p01 >> 16), (uint16_t)p23, (uint16_t)(p23 >> 16)};
+        for (int e = 0; e < 4; ++e)
+          if (o + e < n_out) dst[e] = h[e];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int gq = 0; gq < 4; ++gq) {
     const int n = n0 + 8 * gq + 4 * half;
     float v[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = c[4 * gq + e];
-      if (bias && n + e < N) v[e] = v[e] + __uint_as_float((uint32_t)bias[n + e] << 16);
-    }
+    for (int e = 0; e < 4; ++e) v[e] = c[4 * gq + e];
     uint32_t p01 = pack_bf16x2(v[0], v[1]), p23 = pack_bf16x2(v[2], v[3]);
     if (act == kActGeluTanh) {
       p01 = activate_bf16x2<kActGeluTanh>(p01);

@@ -105,7 +105,9 @@ class Int8RotLinear(nn.Module):
     ``rank``, ``bias`` and ``activation`` are this build's fused extension; with their defaults the module and its
     state dict are exactly the reference's. ``activation="gelu_tanh"`` applies torch's ``gelu(approximate="tanh")``
     to the bf16 output inside the GEMM (a feed-forward up-projection and its activation module in one kernel,
-    transformer.py:75-99); it adds no state.
+    transformer.py:75-99); ``activation="swiglu"`` is the gated feed-forward's input module: the ``out_features``
+    outputs are split in halves and the layer returns ``hidden * silu(gate)``, ``out_features // 2`` wide
+    (``"swiglu_gate_first"``: the gate half first). Activations add no state.
     """
 
     _last_input: ClassVar[dict[str, Any]] = {}
@@ -113,7 +115,8 @@ class Int8RotLinear(nn.Module):
     def __init__(self, in_features: int, out_features: int, group: int, *, rank: int = 0, bias: bool = False,
                  activation: str | None = None) -> None:
         super().__init__()
-        _activation_code(activation)
+        if _activation_code(activation) in _GLU_CODES and out_features % 32:
+            raise ValueError(f"a gated activation needs out_features divisible by 32, got {out_features}")
         self.activation = activation
         if in_features % group:
             raise ValueError(f"in_features {in_features} is not a multiple of the Hadamard group {group}")
@@ -174,7 +177,7 @@ class Int8RotLinear(nn.Module):
                                     activation=self.activation)
         else:
             y = kernels.int8_matmul(xq, self.qweight, sx, self.wscale, bias=self.bias, activation=self.activation)
-        return y.reshape(*shape[:-1], self.out_features).to(x.dtype)
+        return y.reshape(*shape[:-1], y.shape[-1]).to(x.dtype)
 
 
 # ------------------------------------------------------------------------------------------------ device kernels
@@ -269,8 +272,9 @@ def _pad_rank(u: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
     return u.contiguous(), up.contiguous()
 
 
-#: Output activations the GEMM epilogue applies (the C ABI's HF_ACT_* codes).
-ACTIVATIONS = {None: 0, "gelu_tanh": 1}
+#: Output activations the GEMM epilogue applies (the C ABI's HF_ACT_* codes). The gated ones halve the output width.
+ACTIVATIONS = {None: 0, "gelu_tanh": 1, "swiglu": 2, "swiglu_gate_first": 3}
+_GLU_CODES = (2, 3)
 
 
 def _activation_code(activation: str | None) -> int:
@@ -284,12 +288,16 @@ def int8_matmul(a: Tensor, b: Tensor, sa: Tensor, sb: Tensor, *, u: Tensor | Non
     """``bf16((f32(a @ b^T) * sa) * sb [+ u @ up^T] [+ bias])`` for a int8 [M, K], b int8 [N, K] (int8.py:376-390).
 
     ``activation="gelu_tanh"`` then applies torch's ``gelu(approximate="tanh")`` to that bf16 output in the same
-    kernel (rounded to bf16 again), the feed-forward up-projection's activation (transformer.py:75-99)."""
+    kernel (rounded to bf16 again), the feed-forward up-projection's activation (transformer.py:75-99);
+    ``activation="swiglu"`` returns ``bf16(h * bf16(silu(g)))`` of the output's halves ``h, g = out.chunk(2, -1)``
+    ([M, N / 2]; ``"swiglu_gate_first"``: ``g, h``), the gated feed-forward's input module."""
     act = _activation_code(activation)
     M, K = a.shape
     N = b.shape[0]
     if b.shape[1] != K:
         raise ValueError(f"K mismatch: {a.shape} vs {b.shape}")
+    if act in _GLU_CODES and N % 32:
+        raise ValueError(f"a gated activation needs N divisible by 32, got {N}")
     _same_device(a.device, b, sa, sb, u, up, bias)
     a, b = a.contiguous(), b.contiguous()
     sa = sa.to(torch.float32).contiguous()
@@ -300,7 +308,7 @@ def int8_matmul(a: Tensor, b: Tensor, sa: Tensor, sb: Tensor, *, u: Tensor | Non
         r = u.shape[1]
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
-    c = torch.empty(M, N, device=a.device, dtype=torch.bfloat16)
+    c = torch.empty(M, N // 2 if act in _GLU_CODES else N, device=a.device, dtype=torch.bfloat16)
     lib = _native.library()
     with torch.cuda.device(a.device):
         ws, nbytes = _workspace(a.device, lib.hf_int8_linear_ws_bytes(M, N, K))

@@ -117,12 +117,22 @@ int hf_int8_linear_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw
  * rounded to bf16 again, inside the GEMM's epilogue (no extra pass over y):
  *   HF_ACT_NONE       y unchanged (this is hf_int8_linear_ws)
  *   HF_ACT_GELU_TANH  y = bf16(gelu_tanh(y)), gelu_tanh(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in fp32
+ *   HF_ACT_SWIGLU     gated linear unit: the N weight rows are F = N / 2 "hidden" rows followed by F "gate" rows, and
+ *                     the output has F columns, out[m, j] = bf16(y[m, j] * bf16(silu(y[m, F + j]))) with
+ *                     silu(g) = g / (1 + exp(-g)) in fp32 (y[m, j], y[m, F + j] the bf16 linear outputs above); ldy
+ *                     >= F. N must be a multiple of 32 (else HF_ERR_ARGUMENT), and N * ldw (with r > 0 also
+ *                     N * ld_up * 2) must stay below 2^32 bytes (else HF_ERR_SIZE).
+ *   HF_ACT_SWIGLU_GATE_FIRST  the same with the gate rows first: out[m, j] = bf16(y[m, F + j] * bf16(silu(y[m, j]))).
  * Replaces the feed-forward's up-projection followed by its activation module (transformer.py:75-99, the FFN `net`
- * run by ChunkedFeedForward; torch's `gelu(approximate="tanh")` on the bf16 linear output). Any other activation
- * value is HF_ERR_ARGUMENT.
+ * run by ChunkedFeedForward: the model's SwiGLU `net[0]`, a linear 2F wide whose output is split in two halves,
+ * hidden * silu(gate); torch's `gelu(approximate="tanh")` for a GELU feed-forward). The weight keeps its natural
+ * row order: the kernel reads the rows of each hidden/gate pair side by side. Any other activation value is
+ * HF_ERR_ARGUMENT.
  */
 #define HF_ACT_NONE 0
 #define HF_ACT_GELU_TANH 1
+#define HF_ACT_SWIGLU 2
+#define HF_ACT_SWIGLU_GATE_FIRST 3
 int hf_int8_linear_act_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx,
                           const float* sw, const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up,
                           int32_t r, const uint16_t* bias, int32_t activation, uint16_t* y, int64_t ldy, int64_t M,

@@ -15,7 +15,10 @@ numpy closed forms the tests pin it with:
 * ``composition`` — the reference's own composition ``Int8RotLinear(x) + LowRankLinear(x) + bias`` in bf16 tensor
   arithmetic, which is what the fused extension is graded against;
 * ``gelu_tanh`` — the feed-forward's activation module on a bf16 tensor (torch's ``gelu(approximate="tanh")``,
-  applied to the up-projection output, transformer.py:75-99), in float64 and rounded once.
+  applied to the up-projection output, transformer.py:75-99), in float64 and rounded once;
+* ``silu`` / ``swiglu`` — the model's gated feed-forward input module (``ff.net[0]``, run by ChunkedFeedForward,
+  transformer.py:75-99; the module itself is diffusers' ``SwiGLU``, a dependency absent from the reference tree):
+  the bf16 projection output split in halves, ``hidden * silu(gate)`` in bf16 tensor arithmetic.
 
 Every array crossing into C is a contiguous numpy array; bf16 tensors are carried as ``uint16`` bit patterns.
 """
@@ -251,6 +254,30 @@ def gelu_tanh(y_bits: np.ndarray) -> np.ndarray:
     t = np.tanh(inner.astype(np.float64)).astype(np.float32)  # tanh correctly rounded to fp32
     g = np.float32(0.5) * x * (np.float32(1.0) + t)
     return f32_to_bf16(g.astype(np.float32))
+
+
+def silu(x_bits: np.ndarray) -> np.ndarray:
+    """``bf16(x / (1 + exp(-x)))`` of a bf16 tensor, torch's ``silu`` formula evaluated in fp32 (exp correctly
+    rounded to fp32, then the fp32 add and divide), rounded once to bf16."""
+    x = bf16_to_f32(np.asarray(x_bits, dtype=np.uint16)).astype(np.float32)
+    # x below about -88.7: exp(-x) is inf in fp32 and the quotient is -0 (NaN for x = -inf, as in torch)
+    with np.errstate(over="ignore", invalid="ignore"):
+        e = np.exp(-x.astype(np.float64)).astype(np.float32)
+        s = x / (np.float32(1.0) + e)
+    return f32_to_bf16(s.astype(np.float32))
+
+
+def swiglu(y_bits: np.ndarray, gate_first: bool = False) -> np.ndarray:
+    """The gated feed-forward's activation on the bf16 projection output ``y`` [..., 2F]: ``hidden, gate =
+    y.chunk(2, -1)`` (``gate, hidden`` when ``gate_first``), then ``hidden * silu(gate)`` in bf16 tensor arithmetic
+    (the product of two bf16 values is exact in fp32, so one rounding to bf16). Returns [..., F] bf16 bits."""
+    y = np.asarray(y_bits, dtype=np.uint16)
+    f = y.shape[-1] // 2
+    if y.shape[-1] != 2 * f:
+        raise ValueError(f"the projection output width {y.shape[-1]} is odd")
+    first, second = y[..., :f], y[..., f:]
+    hidden, gate = (second, first) if gate_first else (first, second)
+    return f32_to_bf16(bf16_to_f32(hidden) * bf16_to_f32(silu(gate)))
 
 
 # ------------------------------------------------------------------------------------------------ seeded inputs

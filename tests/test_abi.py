@@ -76,9 +76,18 @@ def test_argument_checks_reject_before_launching(lib):
     # an activation code the epilogue does not know, even with nothing to compute
     assert lib.hf_int8_linear_act_ws(fake, 128, fake, 128, fake, fake, null, 0, null, 0, 0, null, 7, fake, 64, 4, 64,
                                      128, null, 0, null) == -1
-    assert lib.hf_int8_linear_act_ws(null, 128, null, 128, null, null, null, 0, null, 0, 0, null, 2, null, 64, 0, 64,
+    assert lib.hf_int8_linear_act_ws(null, 128, null, 128, null, null, null, 0, null, 0, 0, null, 4, null, 64, 0, 64,
                                      128, null, 0, null) == -1
-    assert lib.hf_int8_linear_act_ws(null, 128, null, 128, null, null, null, 0, null, 0, 0, null, 1, null, 64, 0, 64,
-                                     128, null, 0, null) == 0  # known activation, no rows: no-op
+    for act in (1, 2, 3):  # known activation, no rows: no-op
+        assert lib.hf_int8_linear_act_ws(null, 128, null, 128, null, null, null, 0, null, 0, 0, null, act, null, 64, 0,
+                                         64, 128, null, 0, null) == 0
+    # SwiGLU: the width must split into two halves of a multiple of 16; the output is N / 2 wide, so ldy >= N / 2
+    assert lib.hf_int8_linear_act_ws(fake, 128, fake, 128, fake, fake, null, 0, null, 0, 0, null, 2, fake, 64, 4, 48,
+                                     128, null, 0, null) == -1
+    assert lib.hf_int8_linear_act_ws(fake, 128, fake, 128, fake, fake, null, 0, null, 0, 0, null, 3, fake, 16, 4, 64,
+                                     128, null, 0, null) == -1
+    # pair order reads the whole weight through one 32-bit descriptor
+    assert lib.hf_int8_linear_act_ws(fake, 1 << 16, fake, 1 << 16, fake, fake, null, 0, null, 0, 0, null, 2, fake,
+                                     1 << 15, 4, 1 << 16, 128, null, 0, null) == -5
     # sizes beyond the kernels' index range
     assert lib.hf_int8_gemm_i32(fake, 1 << 24, fake, 128, fake, 64, 4, 64, 128, null) == -5

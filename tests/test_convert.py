@@ -258,3 +258,38 @@ def test_fuse_activations_folds_tanh_gelu_into_the_int8_projection():
     assert isinstance(ff.exact, GELU) and isinstance(ff.dense, GELU)
     assert ff.net[2].activation is None
     assert fuse_activations(ff) == []  # idempotent
+
+
+class SwiGLU(nn.Module):
+    """Stand-in with the attributes of a gated feed-forward's input module: `proj` (2F wide), then
+    `hidden * silu(gate)` of its halves."""
+
+    def __init__(self, proj: nn.Module) -> None:
+        super().__init__()
+        self.proj = proj
+
+    def forward(self, x):
+        hidden, gate = self.proj(x).chunk(2, dim=-1)
+        return hidden * nn.functional.silu(gate)
+
+
+def test_fuse_activations_folds_swiglu_into_the_int8_projection():
+    from hyperflow_h3_flash_amd.convert import fuse_activations
+
+    up = Int8RotLinear(64, 256, group=16)
+    ff = nn.Module()
+    ff.net = nn.ModuleList([SwiGLU(up), nn.Dropout(0.0), Int8RotLinear(128, 64, group=16)])
+    ff.odd = SwiGLU(Int8RotLinear(64, 80, group=16))  # halves of 40: not a multiple of 16, stays unfused
+    ff.dense = SwiGLU(nn.Linear(64, 256))  # not an INT8 projection
+    names = fuse_activations(ff)
+    assert names == ["net.0"]
+    assert ff.net[0] is up and up.activation == "swiglu"
+    assert isinstance(ff.odd, SwiGLU) and isinstance(ff.dense, SwiGLU)
+    assert "activation=swiglu" in repr(up)
+    assert fuse_activations(ff) == []
+
+
+def test_gated_activation_needs_a_width_divisible_by_32():
+    with pytest.raises(ValueError, match="32"):
+        Int8RotLinear(64, 80, group=16, activation="swiglu")
+    Int8RotLinear(64, 96, group=16, activation="swiglu_gate_first")

@@ -343,3 +343,55 @@ def test_gelu_tanh_planted_mistake_is_caught(oracle_lib):
     assert (wrong != theirs).sum() > 100
     ours = oracle_lib.gelu_tanh(bits)
     assert np.abs(oracle_lib.bf16_to_f32(ours) - oracle_lib.bf16_to_f32(theirs)).max() < 1e-6
+
+
+def test_silu_matches_torch_on_every_bf16_value(oracle_lib):
+    """The oracle's SiLU against torch's own `silu` on every finite bf16 value."""
+    import torch
+
+    bits = np.arange(65536, dtype=np.uint16)
+    bits = bits[np.isfinite(oracle_lib.bf16_to_f32(bits))]
+    ours = oracle_lib.silu(bits)
+    x = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    theirs = torch.nn.functional.silu(x).view(torch.int16).numpy().view(np.uint16)
+    diff = ours != theirs
+    assert diff.sum() <= 8, diff.sum()
+
+
+def test_swiglu_matches_the_torch_composition(oracle_lib):
+    """`hidden * silu(gate)` of `y.chunk(2, -1)` in torch bf16 tensor arithmetic (the gated feed-forward module),
+    both half orders, against the oracle: bitwise."""
+    import torch
+
+    rng = np.random.default_rng(5)
+    y = oracle_lib.f32_to_bf16((rng.standard_normal((64, 96)) * 4).astype(np.float32))
+    t = torch.from_numpy(y.view(np.int16)).view(torch.bfloat16)
+    first, second = t.chunk(2, dim=-1)
+    for gate_first, (hidden, gate) in ((False, (first, second)), (True, (second, first))):
+        theirs = (hidden * torch.nn.functional.silu(gate)).view(torch.int16).numpy().view(np.uint16)
+        ours = oracle_lib.swiglu(y, gate_first=gate_first)
+        assert ours.shape == (64, 48)
+        assert (ours == theirs).all()
+
+
+def test_silu_closed_forms(oracle_lib):
+    """silu(0) = 0, silu(x) = x for large x, -0 far below zero, silu(1) = 1 / (1 + 1/e) = 0.7310585... (bf16
+    0.73046875), and swiglu of a zero gate is zero."""
+    x = oracle_lib.f32_to_bf16(np.array([0.0, 1.0, 200.0, -200.0], dtype=np.float32))
+    s = oracle_lib.bf16_to_f32(oracle_lib.silu(x))
+    assert s[0] == 0.0 and s[2] == 200.0 and s[3] == 0.0
+    assert s[1] == oracle_lib.bf16_to_f32(oracle_lib.f64_to_bf16(np.array([1.0 / (1.0 + np.exp(-1.0))])))[0]
+    y = oracle_lib.f32_to_bf16(np.array([[3.0, -2.0, 0.0, 0.0]], dtype=np.float32))
+    assert (oracle_lib.bf16_to_f32(oracle_lib.swiglu(y)) == 0.0).all()
+
+
+def test_swiglu_planted_mistake_is_caught(oracle_lib):
+    """Swapped halves (silu of the hidden half) fail the comparison with torch."""
+    import torch
+
+    rng = np.random.default_rng(9)
+    y = oracle_lib.f32_to_bf16((rng.standard_normal((32, 64)) * 2).astype(np.float32))
+    t = torch.from_numpy(y.view(np.int16)).view(torch.bfloat16)
+    hidden, gate = t.chunk(2, dim=-1)
+    theirs = (hidden * torch.nn.functional.silu(gate)).view(torch.int16).numpy().view(np.uint16)
+    assert (oracle_lib.swiglu(y, gate_first=True) != theirs).mean() > 0.5
