@@ -22,6 +22,8 @@ parity-test shapes and supporting measurements, not the headline line):
   6  the model's gated FFN on M=32768: up 5376->28672 (14336 hidden + 14336 gate rows), SwiGLU in bf16, down
      14336->5376, rank 64; timed unfused (torch chunk + silu + multiply between the layers) and fused (SwiGLU in
      the up-projection's GEMM epilogue)
+  7  the model's own linear shapes (K, N) on the 5.2 s clip's M=37710 tokens, rank 64: q/k/v 5376->7168 each,
+     the fused q/k/v 5376->21504, out 7168->5376, gated up 5376->28672, down 14336->5376
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--config N]
 """
@@ -53,8 +55,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=32768, help="row sample for the CPU baseline")
-    p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6),
-                   help="workload: 2 (default) is the headline QKV projection; 1, 3-6 are supporting measurements")
+    p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6, 7),
+                   help="workload: 2 (default) is the headline QKV projection; 1, 3-7 are supporting measurements")
     p.add_argument("--copy-probe", action="store_true",
                    help="only copy a 1 GiB device buffer 3 times (calibrates the HBM byte counters) and exit")
     p.add_argument("--vendor-gemm", action="store_true",
@@ -121,34 +123,37 @@ def read_traffic():
     return None
 
 
-def cpu_baseline(torch, rows, seed=0):
+def cpu_baseline(torch, rows, seed=0, m=M, k=K, n=N, rank=RANK, bias=False):
     """The reference's CPU PyTorch path (int8.py:173-179, restated in oracle/torch_path.py) plus the low-rank
-    composition, on a `rows`-row sample of the workload: 1 warm-up then the median of 3 timed calls."""
+    composition (and a bias), on a `rows`-row sample of an m-row workload: 1 warm-up then the median of 3 timed
+    calls."""
     from oracle import torch_path
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(seed)
-    x = (torch.randn(rows, K, generator=gen)).to(torch.bfloat16)
-    qweight = torch.randint(-127, 128, (N, K), dtype=torch.int8, generator=gen)
-    wscale = torch.rand(N, generator=gen) * 9e-3 + 1e-3
-    down = (torch.randn(RANK, K, generator=gen) * 0.02).to(torch.bfloat16)
-    up = (torch.randn(N, RANK, generator=gen) * 0.02).to(torch.bfloat16)
+    x = (torch.randn(rows, k, generator=gen)).to(torch.bfloat16)
+    qweight = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=gen)
+    wscale = torch.rand(n, generator=gen) * 9e-3 + 1e-3
+    down = (torch.randn(rank, k, generator=gen) * 0.02).to(torch.bfloat16)
+    up = (torch.randn(n, rank, generator=gen) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(n, generator=gen) * 0.01).to(torch.bfloat16) if bias else None
     times = []
     for i in range(4):
         t0 = time.perf_counter()
-        torch_path.forward_torch(x, qweight, wscale, GROUP, down, up)
+        torch_path.forward_torch(x, qweight, wscale, GROUP, down, up, b)
         t = time.perf_counter() - t0
         if i:
             times.append(t)
     t = statistics.median(times)
     return {
-        "value": round(2.0 * rows * N * K / t / 1e12, 4),
+        "value": round(2.0 * rows * n * k / t / 1e12, 4),
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
-        "sample": f"{rows} of {M} rows (K={K}, N={N}, G={GROUP}, rank {RANK}); median of 3 after 1 warm-up, "
-                  f"{t:.2f} s per call; torch {torch.__version__} CPU, {platform.processor() or platform.machine()}",
+        "sample": f"{rows} of {m} rows (K={k}, N={n}, G={GROUP}, rank {rank}{', bias' if bias else ''}); median of "
+                  f"3 after 1 warm-up, {t:.3f} s per call; torch {torch.__version__} CPU, "
+                  f"{platform.processor() or platform.machine()}",
     }
 
 
@@ -317,9 +322,11 @@ def run_config(torch, config, steps, warmup):
         x, (layer,) = layer_inputs(torch, dev, m, k, n, r, True, 0.01, 20.0, seed=1)
         with torch.no_grad():
             t = timed(torch, lambda: layer(x), steps, warmup)
+        # the reference's own CPU-runnable case: its CPU path over all 1024 rows, beside the device figure
+        cpu = cpu_baseline(torch, m, seed=1, m=m, k=k, n=n, rank=r, bias=True)
         yield dict(base, metric="convrot INT8 linear TOPS, M=1024 K=3072 N=3072", unit="TOPS",
                    value=round(2.0 * m * n * k / t / 1e12, 2), ms_per_step=round(t * 1e3, 4), higher_is_better=True,
-                   hbm_GBs=round(linear_bytes(m, k, n, r, True) / t / 1e9, 1),
+                   hbm_GBs=round(linear_bytes(m, k, n, r, True) / t / 1e9, 1), cpu_baseline=cpu,
                    config={"workload": "single convrot linear", "M": m, "K": k, "N": n, "group": GROUP,
                            "rank": r, "bias": True})
     elif config in (3, 4, 6):
@@ -366,6 +373,20 @@ def run_config(torch, config, steps, warmup):
                    config={"workload": name, "M": m, "shapes_KN": shapes, "group": GROUP, "rank": 64,
                            "bias": False,
                            "activation": {3: "fused tanh-GELU epilogue", 6: "fused SwiGLU epilogue"}.get(config)})
+    elif config == 7:
+        m = 37710
+        for name, k, n in (("q/k/v", 5376, 7168), ("fused q/k/v", 5376, 21504), ("out", 7168, 5376),
+                           ("gated up", 5376, 28672), ("down", 14336, 5376)):
+            x, (layer,) = layer_inputs(torch, dev, m, k, n, 64, False, 0.005, 30.0, seed=7)
+            with torch.no_grad():
+                t = timed(torch, lambda: layer(x), steps, warmup)
+            yield dict(base, metric=f"convrot INT8 linear TOPS, model {name} M={m} K={k} N={n}", unit="TOPS",
+                       value=round(2.0 * m * n * k / t / 1e12, 2), ms_per_step=round(t * 1e3, 4),
+                       higher_is_better=True, pct_of_peak=round(100.0 * 2.0 * m * n * k / t / 1e12 / PEAK_INT8_TOPS, 2),
+                       config={"workload": f"model linear ({name})", "M": m, "K": k, "N": n, "group": GROUP,
+                               "rank": 64, "bias": False})
+            del x, layer
+            torch.cuda.empty_cache()
     else:
         k = 5120
         for m in (64, 256, 1024):

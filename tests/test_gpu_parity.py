@@ -106,7 +106,8 @@ def test_rotate_quant_groups_and_partial_tiles(oracle_lib, group, m, k):
 
 
 @pytest.mark.parametrize("m,k", [(3, 14336), (3, 16384), (1025, 1024), (1024, 13824), (2, 77312), (1030, 5120),
-                                 (1100, 5376), (1027, 13824), (1025, 20480), (1025, 21504)])
+                                 (1100, 5376), (1027, 13824), (1025, 20480), (1025, 21504), (1029, 7168),
+                                 (1031, 14336)])
 def test_rotate_quant_both_row_layouts(oracle_lib, m, k):
     """Up to 1024 rows of at most 14 tiles run one workgroup per row. More rows of up to 20 tiles keep the row in
     registers, split over 1 (<= 5 tiles), 2 (6: a partial last tile), 3 (14) or 4 (20) waves per row; wider rows
@@ -269,10 +270,14 @@ def test_lowrank_down_matches_oracle(oracle_lib, rank):
 # ------------------------------------------------------------------------------------------- benchmark-size shapes
 
 
-@pytest.mark.parametrize("m,k,n", [(4096, 5120, 2048), (32768, 5120, 15360)])
+@pytest.mark.parametrize("m,k,n", [(4096, 5120, 2048), (32768, 5120, 15360),
+                                   # the model's own linears: q/k/v, out, the gated FFN's up and down, fused q/k/v
+                                   (4099, 5376, 7168), (4099, 7168, 5376), (2053, 5376, 28672), (2053, 14336, 5376),
+                                   (4099, 5376, 21504)])
 def test_benchmark_shapes_on_sampled_rows(oracle_lib, m, k, n):
     """The full-size layer on the device; the oracle checks a seeded sample of rows (rows are independent), and
-    size-independent properties are checked on every row."""
+    size-independent properties are checked on every row. Also the model's own linear shapes (hidden 5376, attention
+    7168, feed-forward 2 x 14336) with a ragged row count."""
     from hyperflow_h3_flash_amd import Int8RotLinear
     from hyperflow_h3_flash_amd.int8 import rotate_quant
 
