@@ -5,13 +5,16 @@ Importing the package does not touch the GPU or load the HIP library; the first 
 
 from .int8 import (
     ACTIVATIONS,
+    ARITHMETIC_OPTIONS,
     INT8_GEMMS,
     KERNEL_OPTIONS,
+    ROTATE_ARITHMETICS,
     ROTATE_QUANTS,
     Int8RotLinear,
     hadamard_factors,
     regular_hadamard,
     resolve_int8_gemm,
+    set_arithmetic_options,
     set_kernel_options,
 )
 from .lowrank import RANK_MULTIPLE, LowRankLinear, fuse_qkv, set_lowrank_rank_multiple
@@ -20,8 +23,10 @@ __version__ = "0.1.0"
 
 __all__ = [
     "ACTIVATIONS",
+    "ARITHMETIC_OPTIONS",
     "INT8_GEMMS",
     "KERNEL_OPTIONS",
+    "ROTATE_ARITHMETICS",
     "ROTATE_QUANTS",
     "Int8RotLinear",
     "LowRankLinear",
@@ -30,6 +35,7 @@ __all__ = [
     "hadamard_factors",
     "regular_hadamard",
     "resolve_int8_gemm",
+    "set_arithmetic_options",
     "set_kernel_options",
     "set_lowrank_rank_multiple",
 ]

@@ -44,6 +44,7 @@ SIGNATURES = {
     "hf_version": ([], ctypes.c_char_p),
     "hf_strerror": ([ctypes.c_int], ctypes.c_char_p),
     "hf_rotate_quant": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I32, _P], ctypes.c_int),
+    "hf_rotate_quant_ex": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I32, _I32, _P], ctypes.c_int),
     "hf_lowrank_down": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I32, _P], ctypes.c_int),
     "hf_lowrank_down_ws_bytes": ([_I64, _I64, _I32], ctypes.c_int64),
     "hf_lowrank_down_ws": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I32, _P, _I64, _P], ctypes.c_int),

@@ -407,6 +407,30 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
   return launch_status();
 }
 
+int hf_rotate_quant_ex(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int64_t K,
+                       int32_t group, int32_t arithmetic, hf_stream_t stream) {
+  if (arithmetic == HF_ROTATE_BF16_DIV) return hf_rotate_quant(x, ldx, q, ldq, sx, M, K, group, stream);
+  if (arithmetic != HF_ROTATE_F32_RECIP) return HF_ERR_ARGUMENT;
+  if (M < 0 || K <= 0 || ldx < K || ldq < K) return HF_ERR_ARGUMENT;
+  if (M == 0) return HF_OK;
+  if (!x || !q || !sx) return HF_ERR_ARGUMENT;
+  const int lg = log4_of(group);
+  if (lg < 0 || K % group) return HF_ERR_GROUP;
+  if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16)) return HF_ERR_ALIGNMENT;
+  if (K >= (int64_t(1) << 30)) return HF_ERR_SIZE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  constexpr int waves = 4;
+  const size_t lds = hf::rotate_quant_f32_recip_lds_bytes(waves);
+  const unsigned blocks = (unsigned)std::min<int64_t>((M + waves - 1) / waves, int64_t(1) << 30);
+  switch (lg) {
+    case 1: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<1>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    case 2: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<2>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    case 3: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<3>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    default: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<4>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+  }
+  return launch_status();
+}
+
 int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_t ld_down, uint16_t* u,
                     int64_t ldu, int64_t M, int64_t K, int32_t r, hf_stream_t stream) {
   return lowrank_down_impl(x, ldx, down, ld_down, u, ldu, M, K, r, nullptr, 0, stream);

@@ -66,14 +66,11 @@ __device__ __forceinline__ int held_offset(int lane, int i, int h) {
   return 256 * (lane >> 4) + 16 * (2 * i + h) + (lane & 15);
 }
 
-// Rotates one 1024-element tile (this lane's 16 consecutive inputs 16 lane .. 16 lane + 15 in cur0, cur1), rounds
-// every value once to bf16 and returns them as 8 packed pairs (low half first) in the layout of held_offset, with
-// this lane's absmax of the rounded, still unnormalised sums. `scratch` is the wave's fp64 transpose area.
+// Rotates one 1024-element tile (this lane's 16 consecutive inputs 16 lane .. 16 lane + 15 in cur0, cur1): v[2i + h]
+// receives the exact unnormalised sum of value 2i + h of the layout of held_offset. `scratch` is the wave's fp64
+// transpose area.
 template <int LOG4G>
-__device__ __forceinline__ float rotate_tile_packed(uint4 cur0, uint4 cur1, int lane, double* scratch,
-                                                    uint32_t (&packed)[8]) {
-  float amax = 0.0f;
-  double v[16];
+__device__ __forceinline__ void rotate_tile_f64(uint4 cur0, uint4 cur1, int lane, double* scratch, double (&v)[16]) {
   const uint32_t w[8] = {cur0.x, cur0.y, cur0.z, cur0.w, cur1.x, cur1.y, cur1.z, cur1.w};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -110,6 +107,16 @@ __device__ __forceinline__ float rotate_tile_packed(uint4 cur0, uint4 cur1, int 
     }
     wave_lds_sync();  // scratch is rewritten by the next tile
   }
+}
+
+// rotate_tile_f64, then every value rounded once to bf16, returned as 8 packed pairs (low half first) in the layout
+// of held_offset, with this lane's absmax of the rounded, still unnormalised sums.
+template <int LOG4G>
+__device__ __forceinline__ float rotate_tile_packed(uint4 cur0, uint4 cur1, int lane, double* scratch,
+                                                    uint32_t (&packed)[8]) {
+  float amax = 0.0f;
+  double v[16];
+  rotate_tile_f64<LOG4G>(cur0, cur1, lane, scratch, v);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float lo = round_f64_to_bf16_value(v[2 * i]);
@@ -358,6 +365,70 @@ void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t
     }
   }
 }
+
+// The arithmetic of the reference's GPU kernels (rotate_quant_kernel / rotate_quant_factored_kernel,
+// src/hyperflow_h3_flash/int8.py:194-262): the rotated value is the exact sum rounded once to fp32 (not bf16),
+//   sx = max(absmax_row(xr), 1e-12) / 127,  inv = 1 / sx  (fp32),  xq = clamp(rint(fp32(xr * inv)), -127, 127).
+// Two passes over the row like the reference's kernels (the absmax, then the rotation again for the codes): one wave
+// per row, tiles of 1024, the fp64 butterfly of rotate_tile_f64. The 2^-n normalisation is a power of two folded
+// into the scale: fp32(t 2^-n) = fp32(t) 2^-n and xr * inv = fp32(t) * (inv 2^-n) exactly.
+template <int LOG4G>
+__global__ __launch_bounds__(256) void rotate_quant_f32_recip_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                     int8_t* __restrict__ q, int64_t ldq,
+                                                                     float* __restrict__ s, int64_t M, int K) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int waves = blockDim.x >> 6;
+  double* scratch = reinterpret_cast<double*>(smem + (size_t)wave * kRqScratchBytes);
+  unsigned char* stage = reinterpret_cast<unsigned char*>(scratch);
+  const int ntiles = (K + kRqTile - 1) / kRqTile;
+  for (int64_t row = (int64_t)blockIdx.x * waves + wave; row < M; row += (int64_t)gridDim.x * waves) {
+    const uint16_t* xrow = x + row * ldx;
+    float amax = 0.0f;
+    for (int t = 0; t < ntiles; ++t) {
+      uint4 a, b;
+      load_pencil(xrow, t * kRqTile + lane * 16, K, a, b);
+      double v[16];
+      rotate_tile_f64<LOG4G>(a, b, lane, scratch, v);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf((float)v[i]));
+    }
+    const float sx = fmaxf(ldexpf(wave_max(amax), -LOG4G), 1e-12f) / 127.0f;
+    const float inv_n = ldexpf(1.0f / sx, -LOG4G);
+    if (lane == 0) s[row] = sx;
+    int8_t* qrow = q + row * ldq;
+    for (int t = 0; t < ntiles; ++t) {
+      uint4 a, b;
+      load_pencil(xrow, t * kRqTile + lane * 16, K, a, b);
+      double v[16];
+      rotate_tile_f64<LOG4G>(a, b, lane, scratch, v);
+      uint32_t out[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float r = fminf(fmaxf(rintf((float)v[4 * i + j] * inv_n), -127.0f), 127.0f);
+          word |= ((uint32_t)((int)r & 0xff)) << (8 * j);
+        }
+        out[i] = word;
+      }
+      store_quantized_tile<LOG4G>(out, t * kRqTile, K, lane, stage, qrow);
+    }
+  }
+}
+
+size_t rotate_quant_f32_recip_lds_bytes(int waves) { return (size_t)waves * kRqScratchBytes; }
+
+template __global__ void rotate_quant_f32_recip_kernel<1>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t,
+                                                          int);
+template __global__ void rotate_quant_f32_recip_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t,
+                                                          int);
+template __global__ void rotate_quant_f32_recip_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t,
+                                                          int);
+template __global__ void rotate_quant_f32_recip_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t,
+                                                          int);
 
 #define HF_RQ_REG(L, T)                                                                                            \
   template __global__ void rotate_quant_reg_kernel<L, T>(const uint16_t*, int64_t, int8_t*, int64_t, float*,       \

@@ -43,6 +43,13 @@ BACKEND = "hip-gfx950"
 #: Run-time kernel choices for every `Int8RotLinear` (int8.py:45-46).
 KERNEL_OPTIONS: dict[str, Any] = {"int8_gemm": "auto", "rotate_quant": "dense"}
 
+#: The arithmetic of the activation rotation + quantization (this build's option; the C ABI's HF_ROTATE_* codes):
+#: "bf16_div" is the reference's torch path (int8.py:176-178: the rotated value rounded to bf16, a true division),
+#: "f32_recip" the reference's GPU kernels (int8.py:194-262: the rotated value in fp32, a reciprocal multiply), the
+#: arithmetic its pipeline runs on CUDA devices.
+ROTATE_ARITHMETICS = {"bf16_div": 0, "f32_recip": 1}
+ARITHMETIC_OPTIONS: dict[str, Any] = {"rotate_quant": "bf16_div"}
+
 
 def set_kernel_options(*, int8_gemm: str | None = None, rotate_quant: str | None = None) -> None:
     """Validate and store kernel choices (int8.py:49-57): ValueError for names outside the reference's sets."""
@@ -54,6 +61,14 @@ def set_kernel_options(*, int8_gemm: str | None = None, rotate_quant: str | None
         if rotate_quant not in ROTATE_QUANTS:
             raise ValueError(f"rotate_quant must be one of {ROTATE_QUANTS}, got {rotate_quant!r}")
         KERNEL_OPTIONS["rotate_quant"] = rotate_quant
+
+
+def set_arithmetic_options(*, rotate_quant: str | None = None) -> None:
+    """Select the rotation + quantization arithmetic for every later call (ValueError for other names)."""
+    if rotate_quant is not None:
+        if rotate_quant not in ROTATE_ARITHMETICS:
+            raise ValueError(f"rotate_quant arithmetic must be one of {tuple(ROTATE_ARITHMETICS)}, got {rotate_quant!r}")
+        ARITHMETIC_OPTIONS["rotate_quant"] = rotate_quant
 
 
 def resolve_int8_gemm(device: torch.device | None = None) -> str:
@@ -153,11 +168,13 @@ class Int8RotLinear(nn.Module):
         cache = Int8RotLinear._last_input
         # Inference tensors (`torch.inference_mode`) have no version counter.
         version = None if x.is_inference() else x._version
-        hit = cache.get("x") is x and cache.get("version") == version and cache.get("group") == self.group
+        arithmetic = ARITHMETIC_OPTIONS["rotate_quant"]
+        hit = (cache.get("x") is x and cache.get("version") == version and cache.get("group") == self.group
+               and cache.get("arithmetic") == arithmetic)
         quantized = cache["value"] if hit else kernels.rotate_quant(x2, self.group)
         cache.clear()
         if self.keep_input:
-            cache.update(x=x, version=version, group=self.group, value=quantized)
+            cache.update(x=x, version=version, group=self.group, arithmetic=arithmetic, value=quantized)
         return quantized
 
     def forward(self, x: Tensor) -> Tensor:
@@ -213,18 +230,24 @@ def _same_device(device: torch.device, *tensors: Tensor | None) -> None:
             raise ValueError(f"tensor on {t.device}, expected {device}")
 
 
-def rotate_quant(x: Tensor, group: int) -> tuple[Tensor, Tensor]:
-    """(int8 codes [M, K], fp32 per-token scales [M]) of ``x`` (bf16 [M, K], rows contiguous), int8.py:326-344."""
+def rotate_quant(x: Tensor, group: int, arithmetic: str | None = None) -> tuple[Tensor, Tensor]:
+    """(int8 codes [M, K], fp32 per-token scales [M]) of ``x`` (bf16 [M, K], rows contiguous), int8.py:326-344.
+
+    ``arithmetic`` (default ``ARITHMETIC_OPTIONS["rotate_quant"]``): "bf16_div" (the reference's torch path) or
+    "f32_recip" (the reference's GPU kernels)."""
     _check_group(group)
     if x.dtype != torch.bfloat16 or x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("rotate_quant expects a bf16 [M, K] tensor with contiguous rows")
+    arithmetic = ARITHMETIC_OPTIONS["rotate_quant"] if arithmetic is None else arithmetic
+    if arithmetic not in ROTATE_ARITHMETICS:
+        raise ValueError(f"rotate_quant arithmetic must be one of {tuple(ROTATE_ARITHMETICS)}, got {arithmetic!r}")
     M, K = x.shape
     q = torch.empty(M, K, device=x.device, dtype=torch.int8)
     s = torch.empty(M, device=x.device, dtype=torch.float32)
     with torch.cuda.device(x.device):
-        status = _native.library().hf_rotate_quant(_ptr(x), x.stride(0), _ptr(q), q.stride(0), _ptr(s), M, K, group,
-                                                   _stream(x.device))
-    _check(status, "hf_rotate_quant")
+        status = _native.library().hf_rotate_quant_ex(_ptr(x), x.stride(0), _ptr(q), q.stride(0), _ptr(s), M, K,
+                                                      group, ROTATE_ARITHMETICS[arithmetic], _stream(x.device))
+    _check(status, "hf_rotate_quant_ex")
     return q, s
 
 
@@ -352,12 +375,15 @@ def _kernels() -> SimpleNamespace:
 
 __all__ = [
     "ACTIVATIONS",
+    "ARITHMETIC_OPTIONS",
     "INT8_GEMMS",
     "KERNEL_OPTIONS",
+    "ROTATE_ARITHMETICS",
     "ROTATE_QUANTS",
     "Int8RotLinear",
     "hadamard_factors",
     "regular_hadamard",
     "resolve_int8_gemm",
+    "set_arithmetic_options",
     "set_kernel_options",
 ]

@@ -56,6 +56,23 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
                     int32_t group, hf_stream_t stream);
 
 /*
+ * hf_rotate_quant with a choice of arithmetic:
+ *   HF_ROTATE_BF16_DIV   the reference's torch path above (int8.py:176-178); exactly hf_rotate_quant
+ *   HF_ROTATE_F32_RECIP  the reference's GPU kernels (rotate_quant_kernel and rotate_quant_factored_kernel,
+ *                        int8.py:194-262, the arithmetic its pipeline runs on CUDA devices):
+ *                          xr = fp32(x[m, g*G:(g+1)*G] @ H_G)   exact sum, rounded once to nearest even
+ *                          sx[m] = max(max_k |xr[m, k]|, 1e-12) / 127,  inv = 1 / sx[m]   (fp32)
+ *                          q[m, k] = clamp(rint(fp32(xr[m, k] * inv)), -127, 127)
+ *                        Two passes over each row (the absmax, then the codes), as the reference's kernels do.
+ * Same operand rules as hf_rotate_quant (any K below 2^30 for HF_ROTATE_F32_RECIP); any other arithmetic value is
+ * HF_ERR_ARGUMENT. Replaces `rotate_quant(x2, group)` (int8.py:326-344) under the reference's CUDA arithmetic.
+ */
+#define HF_ROTATE_BF16_DIV 0
+#define HF_ROTATE_F32_RECIP 1
+int hf_rotate_quant_ex(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int64_t K,
+                       int32_t group, int32_t arithmetic, hf_stream_t stream);
+
+/*
  * Low-rank down projection u = bf16(x @ down^T) (LowRankLinear's bf16 intermediate, transformer.py:57-58).
  * x: bf16 [M, ldx]; down: bf16 [r, ld_down] (nn.Linear(K, r).weight); u: bf16 [M, ldu].
  * Requires: K % 16 == 0; x, down 16-byte aligned; ldx % 8 == 0; ld_down % 8 == 0; u 8-byte aligned.

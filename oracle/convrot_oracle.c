@@ -130,6 +130,40 @@ static void acc_add_term(superacc* a, uint32_t mant, int exp2, int negative) {
   }
 }
 
+/* Round the exact accumulator value to a float with `bits` significant bits (8: bf16, 24: fp32), nearest even,
+ * with the subnormal quantum 2^qmin_exp; returns the rounded value (exact in a double) or +-inf past 2^128. */
+static double acc_round(const superacc* a, int bits, int qmin_exp) {
+  uint64_t m[ACC_LIMBS];
+  memcpy(m, a->w, sizeof m);
+  int negative = (int64_t)m[ACC_LIMBS - 1] < 0;
+  if (negative) {
+    int carry = 1;
+    for (int k = 0; k < ACC_LIMBS; ++k) {
+      uint64_t v = ~m[k] + (uint64_t)carry;
+      carry = carry && (v == 0);
+      m[k] = v;
+    }
+  }
+  int top = -1;
+  for (int k = ACC_LIMBS - 1; k >= 0 && top < 0; --k)
+    if (m[k]) top = k * 64 + 63 - __builtin_clzll(m[k]);
+  if (top < 0) return 0.0; /* an exact zero sum is +0 */
+  int q = top - (bits - 1);
+  int qmin = qmin_exp - ACC_LSB_EXP;
+  if (q < qmin) q = qmin;
+#define BIT(i) ((i) < 0 ? 0u : (unsigned)((m[(i) >> 6] >> ((i) & 63)) & 1u))
+  uint64_t kept = 0;
+  for (int b = top; b >= q; --b) kept = (kept << 1) | BIT(b);
+  unsigned round = BIT(q - 1);
+  unsigned sticky = 0;
+  for (int b = q - 2; b >= 0 && !sticky; --b) sticky = BIT(b);
+#undef BIT
+  if (round && (sticky || (kept & 1))) kept += 1;
+  double v = ldexp((double)kept, q + ACC_LSB_EXP);
+  if (v >= 0x1p128) v = INFINITY;
+  return negative ? -v : v;
+}
+
 /* Round the exact accumulator value to bf16, nearest even. */
 static uint16_t acc_to_bf16(const superacc* a) {
   uint64_t m[ACC_LIMBS];
@@ -233,6 +267,80 @@ int oracle_rotate(const uint16_t* x, int64_t M, int64_t K, int G, uint16_t* xr, 
   free(xd);
   free(neg);
   return 0;
+}
+
+/* The reference's GPU kernels' rotation (rotate_quant_kernel and rotate_quant_factored_kernel, int8.py:194-262):
+ * the same exact sum, rounded once to fp32 instead of bf16 (their fp32 dot products; the factored kernel's 3-term
+ * bf16 split makes its second product exact). */
+int oracle_rotate_f32(const uint16_t* x, int64_t M, int64_t K, int G, float* xr, int force_exact) {
+  int n = 0;
+  while ((1 << (2 * n)) < G) ++n;
+  if ((1 << (2 * n)) != G || K % G) return -1;
+  char* neg = (char*)malloc((size_t)G * G);
+  for (int i = 0; i < G; ++i)
+    for (int j = 0; j < G; ++j) neg[(size_t)i * G + j] = (char)hadamard_negative(i, j, n);
+  double* xd = (double*)malloc(sizeof(double) * G);
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t g0 = 0; g0 < K; g0 += G) {
+      const uint16_t* xg = x + m * K + g0;
+      int emin = 1 << 20, emax = -(1 << 20), nonfinite = 0;
+      for (int i = 0; i < G; ++i) {
+        uint32_t mt;
+        int ex, ng;
+        int kind = bf16_decompose(xg[i], &mt, &ex, &ng);
+        if (kind < 0) nonfinite = 1;
+        if (kind > 0) {
+          if (ex < emin) emin = ex;
+          if (ex > emax) emax = ex;
+        }
+        xd[i] = (double)bf16_to_f32(xg[i]);
+      }
+      int fast = !force_exact && (nonfinite || emax - emin <= 32);
+      for (int j = 0; j < G; ++j) {
+        if (fast) {
+          double s = 0.0;
+          for (int i = 0; i < G; ++i) s += neg[(size_t)i * G + j] ? -xd[i] : xd[i];
+          xr[m * K + g0 + j] = (float)ldexp(s, -n); /* the exact sum, rounded once */
+        } else {
+          superacc a;
+          memset(&a, 0, sizeof a);
+          for (int i = 0; i < G; ++i) {
+            uint32_t mt;
+            int ex, ng;
+            if (bf16_decompose(xg[i], &mt, &ex, &ng) <= 0) continue;
+            acc_add_term(&a, mt, ex - n, ng ^ neg[(size_t)i * G + j]);
+          }
+          xr[m * K + g0 + j] = (float)acc_round(&a, 24, -149);
+        }
+      }
+    }
+  }
+  free(xd);
+  free(neg);
+  return 0;
+}
+
+/* The GPU kernels' quantization (int8.py:208-220): scale = max(amax, 1e-12) / 127 and inv = 1 / scale in fp32,
+ * q = clamp(rint(fp32(v * inv)), -127, 127) (a reciprocal multiply, not a division). */
+void oracle_quantize_recip(const float* xr, int64_t M, int64_t K, float* sx, int8_t* xq) {
+  for (int64_t m = 0; m < M; ++m) {
+    const float* row = xr + m * K;
+    float amax = 0.0f;
+    for (int64_t k = 0; k < K; ++k) {
+      float v = fabsf(row[k]);
+      if (v > amax || isnan(v)) amax = v;
+    }
+    float s = (amax > 1e-12f ? amax : 1e-12f) / 127.0f; /* tl.maximum(amax, 1e-12) / 127.0 */
+    float inv = 1.0f / s;
+    sx[m] = s;
+    for (int64_t k = 0; k < K; ++k) {
+      float t = row[k] * inv;
+      float r = rintf(t);
+      if (r < -127.0f) r = -127.0f;
+      if (r > 127.0f) r = 127.0f;
+      xq[m * K + k] = (int8_t)r;
+    }
+  }
 }
 
 /* ---------------------------------------------------------------- per-token quantization, int8.py:177-178 */

@@ -11,6 +11,9 @@ numpy closed forms the tests pin it with:
 * ``hadamard_factors`` — int8.py:112-119;
 * ``quantize_weight`` — the checkpoint quantizer of tests/test_int8.py:31-36 (float64);
 * ``rotate`` / ``quantize`` / ``int8_gemm`` / ``epilogue`` — int8.py:176-179 step by step;
+* ``rotate_f32`` / ``quantize_recip`` — the arithmetic of the reference's GPU rotate+quantize kernels
+  (int8.py:194-262): the exact rotation rounded to fp32 (not bf16) and a reciprocal multiply (not a division).
+  Pinned by exact arithmetic; parity against those CUDA kernels' own outputs is unpinned (no fixture holds them);
 * ``lowrank_down`` / ``fused_epilogue`` — LowRankLinear (src/hyperflow_h3_flash/transformer.py:57-58) and a bias;
 * ``composition`` — the reference's own composition ``Int8RotLinear(x) + LowRankLinear(x) + bias`` in bf16 tensor
   arithmetic, which is what the fused extension is graded against;
@@ -51,6 +54,8 @@ def _lib() -> ctypes.CDLL:
     lib.oracle_regular_hadamard.argtypes = [i32, p]
     lib.oracle_rotate.argtypes = [p, i64, i64, i32, p, i32]
     lib.oracle_quantize.argtypes = [p, i64, i64, p, p]
+    lib.oracle_rotate_f32.argtypes = [p, i64, i64, i32, p, i32]
+    lib.oracle_quantize_recip.argtypes = [p, i64, i64, p, p]
     lib.oracle_int8_gemm.argtypes = [p, p, i64, i64, i64, p]
     lib.oracle_epilogue.argtypes = [p, p, p, i64, i64, p]
     lib.oracle_lowrank_down.argtypes = [p, p, i64, i64, i64, p]
@@ -157,6 +162,27 @@ def quantize(xr_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     sx = np.empty(m, dtype=np.float32)
     xq = np.empty((m, k), dtype=np.int8)
     _lib().oracle_quantize(_ptr(xr), m, k, _ptr(sx), _ptr(xq))
+    return sx, xq
+
+
+def rotate_f32(x_bits: np.ndarray, group: int, *, force_exact: bool = False) -> np.ndarray:
+    """The reference's GPU rotation (int8.py:194-262): the exact ``x.view(M, K/G, G) @ R`` rounded once to fp32."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    m, k = x.shape
+    out = np.empty((m, k), dtype=np.float32)
+    if _lib().oracle_rotate_f32(_ptr(x), m, k, group, _ptr(out), int(force_exact)) != 0:
+        raise ValueError(f"bad rotation shape K={k} group={group}")
+    return out
+
+
+def quantize_recip(xr: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The reference's GPU quantization (int8.py:208-220): ``s = max(amax, 1e-12) / 127``, ``inv = 1 / s`` and
+    ``q = clamp(rint(v * inv), -127, 127)`` in fp32 on the fp32 rotated values. Returns (sx [M], xq int8 [M, K])."""
+    v = np.ascontiguousarray(xr, dtype=np.float32)
+    m, k = v.shape
+    sx = np.empty(m, dtype=np.float32)
+    xq = np.empty((m, k), dtype=np.int8)
+    _lib().oracle_quantize_recip(_ptr(v), m, k, _ptr(sx), _ptr(xq))
     return sx, xq
 
 

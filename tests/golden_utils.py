@@ -46,6 +46,24 @@ def fraction_to_bf16(v: Fraction) -> int:
     return sign | int(f.view(np.uint32)[0] >> 16)
 
 
+def fraction_to_f32(v: Fraction) -> float:
+    """Round an exact rational to fp32 (nearest, ties to even) with Python's exact Fraction arithmetic."""
+    if v == 0:
+        return 0.0
+    sign = -1.0 if v < 0 else 1.0
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    q = max(e - 23, -149)
+    quantum = Fraction(2) ** q
+    k = round(a / quantum)  # Fraction.__round__ rounds half to even
+    value = k * quantum
+    if value >= Fraction(2) ** 128:
+        return sign * float("inf")
+    return sign * float(np.float32(float(value)))
+
+
 def hadamard_column_signs(group: int, j: int) -> np.ndarray:
     """Signs of column j of the unnormalised regular Hadamard (-1 where an odd number of base-4 digit pairs sum
     to 3)."""

@@ -59,6 +59,12 @@ def test_argument_checks_reject_before_launching(lib):
     # misaligned pointer, K not a multiple of 16
     assert lib.hf_rotate_quant(odd, 256, fake, 256, fake, 4, 256, 256, null) == -3
     assert lib.hf_rotate_quant(fake, 8, fake, 8, fake, 4, 8, 4, null) == -3
+    # the arithmetic selector: unknown codes are rejected; both known codes check operands the same way
+    assert lib.hf_rotate_quant_ex(fake, 256, fake, 256, fake, 4, 256, 256, 2, null) == -1
+    for arith in (0, 1):
+        assert lib.hf_rotate_quant_ex(null, 256, null, 256, null, 0, 256, 256, arith, null) == 0
+        assert lib.hf_rotate_quant_ex(fake, 256, fake, 256, fake, 4, 256, 32, arith, null) == -2
+        assert lib.hf_rotate_quant_ex(odd, 256, fake, 256, fake, 4, 256, 256, arith, null) == -3
     # GEMM: stride smaller than K, misaligned stride, low-rank rank not a multiple of 8
     assert lib.hf_int8_linear(fake, 64, fake, 128, fake, fake, null, 0, null, 0, 0, null, fake, 64, 4, 64, 128,
                               null) == -1

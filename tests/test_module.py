@@ -113,6 +113,37 @@ def test_kernel_options_are_checked_and_default_to_the_release_arithmetic():
         KERNEL_OPTIONS.update(saved)
 
 
+def test_arithmetic_options_are_checked_and_default_to_the_torch_path():
+    from hyperflow_h3_flash_amd import ARITHMETIC_OPTIONS, ROTATE_ARITHMETICS, set_arithmetic_options
+
+    assert ARITHMETIC_OPTIONS == {"rotate_quant": "bf16_div"}
+    assert ROTATE_ARITHMETICS == {"bf16_div": 0, "f32_recip": 1}  # the C ABI's HF_ROTATE_* codes
+    with pytest.raises(ValueError, match="arithmetic"):
+        set_arithmetic_options(rotate_quant="dense")
+    try:
+        set_arithmetic_options(rotate_quant="f32_recip")
+        assert ARITHMETIC_OPTIONS["rotate_quant"] == "f32_recip"
+    finally:
+        set_arithmetic_options(rotate_quant="bf16_div")
+
+
+def test_shared_quantization_is_not_reused_across_arithmetics():
+    from hyperflow_h3_flash_amd import set_arithmetic_options
+
+    calls = []
+    kernels = SimpleNamespace(rotate_quant=lambda x2, group: calls.append(1) or (x2, group))
+    to_q, to_k = Int8RotLinear(16, 16, group=16), Int8RotLinear(16, 16, group=16)
+    to_q.keep_input = True
+    x = torch.randn(4, 16)
+    to_q._quantize(x, x, kernels)
+    try:
+        set_arithmetic_options(rotate_quant="f32_recip")
+        to_k._quantize(x, x, kernels)
+    finally:
+        set_arithmetic_options(rotate_quant="bf16_div")
+    assert len(calls) == 2 and not Int8RotLinear._last_input
+
+
 def test_shared_quantization_works_under_inference_mode():
     calls = []
     kernels = SimpleNamespace(rotate_quant=lambda x2, group: calls.append(1) or (x2, group))

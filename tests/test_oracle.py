@@ -10,7 +10,7 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-from golden_utils import classify_rotation_mismatches, fixture_names, fraction_to_bf16, load_fixture
+from golden_utils import classify_rotation_mismatches, fixture_names, fraction_to_bf16, fraction_to_f32, load_fixture
 
 FIXTURES = fixture_names()
 
@@ -135,6 +135,104 @@ def test_quantize_divides_rather_than_multiplying_by_the_reciprocal(oracle_lib):
     xr = _bits([[amax, a]])
     sx, xq = oracle_lib.quantize(xr)
     assert xq[0, 1] == np.rint(np.float32(a / sx[0]))
+
+
+# ---------------------------------------------- the reference's GPU-kernel arithmetic (int8.py:194-262): fp32, 1/s
+# No golden vectors exist for it (the reference's Triton kernels need CUDA): the restatement is pinned by exact
+# arithmetic and by the cases that separate it from the torch path.
+
+
+@pytest.mark.parametrize("group", [4, 16, 64])
+def test_rotation_f32_is_the_exact_sum_rounded_once(oracle_lib, group):
+    """Brute force in exact rational arithmetic on inputs spanning up to ~250 binades, both summation paths."""
+    rng = np.random.default_rng(100 + group)
+    rows = []
+    for _ in range(5):
+        mags = rng.standard_normal(group) * np.exp2(rng.integers(-60, 60, size=group).astype(np.float64))
+        mags[rng.random(group) < 0.1] = 0.0
+        rows.append(mags)
+    rows.append(rng.standard_normal(group) * 3.0)  # a narrow span: the float64 path
+    x = _bits(np.array(rows, dtype=np.float64).astype(np.float32))
+    got_exact = oracle_lib.rotate_f32(x, group, force_exact=True)
+    got_fast = oracle_lib.rotate_f32(x, group)
+    h = oracle_lib.regular_hadamard(group)
+    for r in range(x.shape[0]):
+        xv = [Fraction(float(v)) for v in oracle_lib.bf16_to_f32(x[r])]
+        for j in range(group):
+            exact = sum((xv[i] * Fraction(h[i, j]) for i in range(group)), Fraction(0))
+            want = fraction_to_f32(exact)
+            assert float(got_exact[r, j]) == want, (r, j)
+            assert float(got_fast[r, j]) == want, (r, j)
+
+
+def test_rotation_f32_rounds_ties_to_even(oracle_lib):
+    # G=4: out_0 = (x0 + x1 + x2 - x3) / 2. (1 + 2^-24)/2 = 0.5 + 2^-25 is the midpoint between 0.5 (even) and
+    # 0.5 + 2^-24; (1 + 3*2^-24)/2 is the midpoint between 0.5 + 2^-24 (odd) and 0.5 + 2^-23 (even).
+    x = _bits([[1.0, 2.0**-24, 0.0, 0.0], [1.0, 3 * 2.0**-24, 0.0, 0.0]])
+    for exact in (True, False):
+        out = oracle_lib.rotate_f32(x, 4, force_exact=exact)
+        assert out[0, 0] == np.float32(0.5) and out[1, 0] == np.float32(0.5 + 2.0**-23)
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_rotation_f32_and_bf16_agree_after_bf16_rounding(oracle_lib, name):
+    """Rounding the fp32 rotation to bf16 gives the bf16 rotation except where the fp32 rounding lands exactly on a
+    bf16 midpoint (a double rounding), which the exact sums show."""
+    f = load_fixture(name)
+    x = f["x"][:16]
+    f32 = oracle_lib.rotate_f32(x, f["G"])
+    b16 = oracle_lib.rotate(x, f["G"])
+    again = oracle_lib.f32_to_bf16(f32)
+    bad = again != b16
+    ties = (f32.view(np.uint32) & 0xFFFF) == 0x8000
+    assert not (bad & ~ties).any()
+
+
+def test_quantize_recip_multiplies_by_the_reciprocal(oracle_lib):
+    """The case that separates a * (1/s) from a / s (the torch path's division): the GPU-kernel quantization takes
+    the reciprocal product."""
+    found = None
+    for amax_q in range(100, 3000):
+        amax = np.float32(amax_q) * np.float32(2.0**-7)
+        s = np.float32(amax / np.float32(127.0))
+        inv = np.float32(np.float32(1.0) / s)
+        for num in range(1, 400):
+            a = np.float32(num) * np.float32(2.0**-7)
+            if a > amax:
+                break
+            if np.rint(np.float32(a / s)) != np.rint(np.float32(a * inv)):
+                found = (amax, a)
+                break
+        if found:
+            break
+    assert found
+    amax, a = found
+    sx, xq = oracle_lib.quantize_recip(np.array([[amax, a]], dtype=np.float32))
+    inv = np.float32(np.float32(1.0) / sx[0])
+    assert xq[0, 1] == np.rint(np.float32(a * inv)) and xq[0, 1] != np.rint(np.float32(a / sx[0]))
+
+
+def test_quantize_recip_zero_row_ties_and_extremes(oracle_lib):
+    # zero row: scale 1e-12 / 127 and zero codes; amax 127 gives s = 1 and inv = 1, so the halves tie to even
+    xr = np.array([[0.0] * 8, [127.0, 2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5]], dtype=np.float32)
+    sx, xq = oracle_lib.quantize_recip(xr)
+    assert sx[0] == np.float32(np.float32(1e-12) / np.float32(127.0)) and not xq[0].any()
+    assert sx[1] == 1.0 and xq[1].tolist() == [127, 2, 4, -2, -4, 0, 2, 0]
+    # every nonzero row reaches +-127 at its absmax and no code leaves [-127, 127]
+    f = load_fixture(FIXTURES[0])
+    sx, xq = oracle_lib.quantize_recip(oracle_lib.rotate_f32(f["x"], f["G"]))
+    assert (np.abs(xq.astype(np.int32)).max(axis=1) == 127).all()
+
+
+def test_gpu_kernel_arithmetic_differs_from_the_torch_path(oracle_lib):
+    """A planted swap of the two arithmetics is visible: on benchmark-like rows every scale and a few percent of the
+    codes differ (each by one)."""
+    inp = oracle_lib.make_inputs(64, 5120, 8, 256, outlier_frac=0.005, outlier_scale=30.0, seed=3)
+    sx_t, xq_t = oracle_lib.quantize(oracle_lib.rotate(inp["x"], 256))
+    sx_k, xq_k = oracle_lib.quantize_recip(oracle_lib.rotate_f32(inp["x"], 256))
+    assert (sx_t != sx_k).mean() > 0.5
+    diff = xq_t.astype(np.int32) - xq_k.astype(np.int32)
+    assert 0.005 < (diff != 0).mean() < 0.2 and np.abs(diff).max() == 1
 
 
 # ------------------------------------------------------------------------------------ GEMM and epilogue (int8.py:179)
