@@ -127,6 +127,15 @@ __device__ __forceinline__ int swizzle128(int r, int c) {  // 128-byte rows: 8 c
   return c ^ ((r ^ (r >> 3)) & 7);
 }
 
+// Split-K partial planes are stored block by block: the int32 accumulators of the 32 x 32 block (bm, bn) of a plane
+// with nbn = ceil(N / 32) block columns occupy the 1024 ints at (bm * nbn + bn) * 1024, in the layout of
+// v_mfma_i32_32x32x32_i8 with the weight as the first operand (lane l: row 32 bm + l % 32; value v: column
+// 32 bn + 8 (v / 4) + 4 (l / 32) + v % 4): values 4g .. 4g + 3 of lane l at 256 g + 4 l, so each of a wave's four
+// 16-byte stores or loads per block covers 1 KiB of contiguous memory. Blocks past M or N are never read.
+__device__ __forceinline__ int64_t partial_block_offset(int bm, int bn, int nbn) {
+  return ((int64_t)bm * nbn + bn) * 1024;
+}
+
 // Buffer resource for raw (stride 0) buffer loads: offsets at or beyond `bytes` read as zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);

@@ -35,6 +35,8 @@ void allow_large_lds() {
   std::call_once(once, [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutI32>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutI32, hf::kActSwiGLU>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16Lr>),
@@ -69,7 +71,9 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLrLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_up_kernel),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kUpLds);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel<false>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kSkinnyLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel<true>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kSkinnyLds);
     (void)hipGetLastError();
   });
@@ -131,7 +135,10 @@ int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream, int act = hf::kAc
   if (tiles >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   const dim3 grid((unsigned)gemm_grid(tiles)), block(hf::kThreads);
   if (i32) {
-    hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutI32>, grid, block, hf::kGemmLds, stream, a);
+    if (act == hf::kActSwiGLU)  // split-K partials in pair order
+      hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutI32, hf::kActSwiGLU>), grid, block, hf::kGemmLds, stream, a);
+    else
+      hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutI32>, grid, block, hf::kGemmLds, stream, a);
   } else if (a.r > 0 && a.r <= 64) {
     if (act == hf::kActGeluTanh)
       hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActGeluTanh>), grid, block, hf::kGemmLds, stream, a);
@@ -270,10 +277,12 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
   return best;
 }
 
+// Ints per split-K partial plane: ceil(M / 32) x ceil(N / 32) blocks of 32 x 32 (partial_block_offset).
+int64_t partial_plane_ints(int64_t M, int64_t N) { return ((M + 31) / 32) * ((N + 31) / 32) * 1024; }
+
 int64_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
   const GemmPlan p = gemm_plan(M, N, K);
-  const int64_t ld = (N + 3) / 4 * 4;
-  return (p.splits > 1 || p.skinny) ? (int64_t)p.splits * M * ld * 4 : 0;
+  return (p.splits > 1 || p.skinny) ? (int64_t)p.splits * partial_plane_ints(M, N) * 4 : 0;
 }
 
 int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
@@ -301,22 +310,28 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
   const int glu_half = (int)(N / 2), glu_gate_first = act_code == HF_ACT_SWIGLU_GATE_FIRST;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const GemmPlan plan = gemm_plan(M, N, K);
-  const int64_t ld_acc = (N + 3) / 4 * 4;
-  if ((plan.splits > 1 || plan.skinny) && ws && aligned(ws, 16) &&
-      ws_bytes >= (int64_t)plan.splits * M * ld_acc * 4) {
-    // Split K: int32 partial planes, then one pass that adds them and applies the epilogue.
+  const int64_t plane = partial_plane_ints(M, N);
+  if ((plan.splits > 1 || plan.skinny) && ws && aligned(ws, 16) && ws_bytes >= (int64_t)plan.splits * plane * 4) {
+    // Split K: int32 partial planes (block by block; in pair order with SwiGLU), then one pass that adds them and
+    // applies the epilogue.
     if (plan.skinny) {
       allow_large_lds();
       const dim3 grid((unsigned)((N + hf::kSkinnyN - 1) / hf::kSkinnyN), (unsigned)plan.splits);
-      hipLaunchKernelGGL(hf::skinny_gemm_kernel, grid, dim3(256), hf::kSkinnyLds, s, q, ldq, w, ldw,
-                         static_cast<int32_t*>(ws), ld_acc, M * ld_acc, (int)M, (int)N, (int)K, plan.k_chunk);
+      if (glu)
+        hipLaunchKernelGGL(hf::skinny_gemm_kernel<true>, grid, dim3(256), hf::kSkinnyLds, s, q, ldq, w, ldw,
+                           static_cast<int32_t*>(ws), plane, (int)M, (int)N, (int)K, plan.k_chunk, glu_half,
+                           glu_gate_first);
+      else
+        hipLaunchKernelGGL(hf::skinny_gemm_kernel<false>, grid, dim3(256), hf::kSkinnyLds, s, q, ldq, w, ldw,
+                           static_cast<int32_t*>(ws), plane, (int)M, (int)N, (int)K, plan.k_chunk, 0, 0);
       st = launch_status();
     } else {
       hf::GemmArgs a{};
-      a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.out = ws; a.ldo = ld_acc;
+      a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.out = ws; a.ldo = 0;
       a.M = (int)M; a.N = (int)N; a.K = (int)K; a.out_vec16 = 1;
-      a.splits = plan.splits; a.k_chunk = plan.k_chunk; a.split_stride = M * ld_acc;
-      st = launch_gemm(a, true, s);
+      a.splits = plan.splits; a.k_chunk = plan.k_chunk; a.split_stride = plane;
+      a.glu_half = glu_half; a.glu_gate_first = glu_gate_first;
+      st = launch_gemm(a, true, s, act);
     }
     if (st != HF_OK) return st;
     const int64_t tiles_n = (N + hf::kSkTileN - 1) / hf::kSkTileN;
@@ -324,9 +339,9 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
     if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;
     const int vec = aligned(y, 8) && (ldy % 4) == 0;
     hipLaunchKernelGGL(hf::splitk_epilogue_kernel, dim3((unsigned)blocks), dim3(64), 0, s,
-                       static_cast<const int32_t*>(ws), ld_acc, M * ld_acc, plan.splits, sx, sw, r > 0 ? u : nullptr,
-                       ldu, r > 0 ? up : nullptr, ld_up, r, bias, y, ldy, (int)M, (int)N, (int)tiles_n, vec, act,
-                       glu_half, glu_gate_first);
+                       static_cast<const int32_t*>(ws), plane, plan.splits, sx, sw, r > 0 ? u : nullptr, ldu,
+                       r > 0 ? up : nullptr, ld_up, r, bias, y, ldy, (int)M, (int)N, (int)tiles_n, vec, act, glu_half,
+                       glu_gate_first);
     return launch_status();
   }
   hf::GemmArgs a{};

@@ -73,7 +73,8 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int out_vec16;         // bf16 rows may be written 16 bytes at a time (16-byte aligned base and ldo % 8 == 0)
   // Split K (int32 output only): work item w covers tile w % tiles and K bytes [s * k_chunk, (s + 1) * k_chunk) with
-  // s = w / tiles, and writes its partial accumulators to plane s, split_stride elements after plane s - 1.
+  // s = w / tiles, and writes its partial accumulators to plane s, split_stride elements after plane s - 1, block by
+  // block (partial_block_offset, nbn = ceil(N / 32); the planes hold ceil(M / 32) x nbn whole blocks).
   int splits;            // 1: no split
   int k_chunk;           // multiple of GBK
   int64_t split_stride;
@@ -268,7 +269,8 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   constexpr bool kGlu = ACT == kActSwiGLU;  // pair order (the glu fields of GemmArgs)
   // Stores per wave of a full tile, when the wait for the next stage 0 behind them fits the 6-bit wait counter
   // (else they are drained).
-  constexpr int kTileStores = GBM * GBN * (OUT == kOutI32 ? 4 : 2) / (ACT == kActSwiGLU ? 2 : 1) / (kWaves * 1024);
+  constexpr int kTileStores =
+      GBM * GBN * (OUT == kOutI32 ? 4 : 2) / (ACT == kActSwiGLU && OUT != kOutI32 ? 2 : 1) / (kWaves * 1024);
   constexpr int kFastStores = kTileStores + kStageLoads <= 63 ? kTileStores : 0;
   float HF_LDS* params = (float HF_LDS*)(smem + kRingBytes);
   const int pt = threadIdx.x & 255;
@@ -425,7 +427,28 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
     bool full;
     if constexpr (OUT == kOutI32) {
       full = cur.rows_m == GBM && cur.rows_n == GBN && a.out_vec16;
-      int32_t* out = static_cast<int32_t*>(a.out) + cur.split * a.split_stride;
+      if (a.splits > 1) {
+        // Split-K partial plane, block by block: every block that starts inside the matrix is written whole (four
+        // 1 KiB contiguous stores per wave); the stores are a fixed count only for a full tile.
+        int32_t* plane = static_cast<int32_t*>(a.out) + cur.split * a.split_stride;
+        const int nbn = (a.N + 31) / 32;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          const int bm = (m0 + wm * 128) / 32 + jb;
+#pragma unroll
+          for (int ib = 0; ib < NB; ++ib) {
+            const int bn = (n0 + wn * WN) / 32 + ib;
+            if (32 * bm < a.M && 32 * bn < a.N) {
+              v4i* dst = reinterpret_cast<v4i*>(plane + partial_block_offset(bm, bn, nbn) + 4 * el);
+              const v16i& c = acc[ib][jb];
+#pragma unroll
+              for (int gq = 0; gq < 4; ++gq)
+                dst[64 * gq] = (v4i){c[4 * gq], c[4 * gq + 1], c[4 * gq + 2], c[4 * gq + 3]};
+            }
+          }
+        }
+      } else {
+      int32_t* out = static_cast<int32_t*>(a.out);
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         const int m = m0 + wm * 128 + jb * 32 + esub;
@@ -447,6 +470,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
               }
             }
           }
+      }
       }
     } else {
       full = cur.rows_m == GBM && cur.rows_n == GBN && a.out_vec16 && (kLr || a.r == 0);
@@ -697,6 +721,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
 }
 
 template __global__ void int8_gemm_kernel<kOutI32>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutI32, kActSwiGLU>(GemmArgs);  // split-K partials in pair order
 template __global__ void int8_gemm_kernel<kOutBf16>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16Lr>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16, kActGeluTanh>(GemmArgs);

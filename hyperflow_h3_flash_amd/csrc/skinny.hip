@@ -1,6 +1,6 @@
 // INT8 x INT8 -> INT32 partial products for at most 64 rows (timestep / text-conditioning modulation, short audio
 // streams): the accumulator of int8_mm_kernel (src/hyperflow_h3_flash/int8.py:302-306) for a K chunk, written as an
-// int32 plane that splitk_epilogue_kernel adds up and finishes.
+// int32 plane (block by block, partial_block_offset) that splitk_epilogue_kernel adds up and finishes.
 //
 // With M <= 64 the weight stream is all the traffic (N x K bytes against 64 x K of activations), so the work is cut
 // into many small weight slices: a work item is 128 weight rows x one K chunk (blockIdx.x = n tile, blockIdx.y =
@@ -24,10 +24,13 @@ constexpr int kSkinnyLoads = 6;                       // per wave and stage: 4 w
 
 __device__ __forceinline__ int skinny_swz(int r) { return (r & 7) ^ ((r >> 3) & 3); }
 
+// GLU: the weight rows are read in pair order (tile column n is weight row glu_row(n, glu_half, glu_gate_first)),
+// the order the split-K epilogue's SwiGLU pairs columns in.
+template <bool GLU>
 __global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __restrict__ q, int64_t ldq,
                                                              const int8_t* __restrict__ w, int64_t ldw,
-                                                             int32_t* __restrict__ acc, int64_t ld_acc,
-                                                             int64_t plane, int M, int N, int K, int k_chunk) {
+                                                             int32_t* __restrict__ acc, int64_t plane, int M, int N,
+                                                             int K, int k_chunk, int glu_half, int glu_gate_first) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char sk_smem_raw[];
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)sk_smem_raw;
   const int lane = threadIdx.x & 63;
@@ -37,8 +40,9 @@ __global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __res
   const int k_lo = blockIdx.y * k_chunk;
   const int k_len = min(K - k_lo, k_chunk);
   const int rows_n = min(kSkinnyN, N - n0);
-  const uint32_t bytes_w = (uint32_t)(rows_n * ldw), bytes_q = (uint32_t)(M * ldq);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + (int64_t)n0 * ldw + k_lo, bytes_w - (uint32_t)k_lo);
+  // Pair order scatters the tile's rows over both halves of the weight: one descriptor for all of it.
+  const uint32_t bytes_w = (uint32_t)((GLU ? N : rows_n) * ldw), bytes_q = (uint32_t)(M * ldq);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + (GLU ? 0 : (int64_t)n0 * ldw) + k_lo, bytes_w - (uint32_t)k_lo);
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + k_lo, bytes_q - (uint32_t)k_lo);
 
   // Stage t -> slot t % 3. Every stage issues 6 loads per wave, stages past the chunk read zeros, so "stage t has
@@ -55,7 +59,9 @@ __global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __res
       const int64_t ld = isq ? ldq : ldw;
       const int rows_valid = isq ? M : rows_n;
       const uint32_t oob = isq ? bytes_q : bytes_w;
-      const uint32_t voff = ((row < rows_valid) & (k0 + c * 16 < k_len)) ? (uint32_t)(row * ld + k0 + c * 16) : oob;
+      // the source row: eight consecutive tile rows from a multiple of 8 are eight consecutive weight rows
+      const int src = (GLU && !isq) ? glu_row(n0 + 8 * blk, glu_half, glu_gate_first) + (lane >> 3) : row;
+      const uint32_t voff = ((row < rows_valid) & (k0 + c * 16 < k_len)) ? (uint32_t)(src * ld + k0 + c * 16) : oob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(isq ? rq : rw,
                                                (void HF_LDS*)(st + (isq ? kSkinnyWBytes : 0) + blk * 1024), 16, voff,
                                                0, 0, 0);
@@ -87,25 +93,24 @@ __global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __res
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // zero-fill loads past the chunk may still be landing
 
-  // Lane (sub, h) holds row m = 32jb + sub, columns n0 + 32w + 8g + 4h + (0..3) in registers 4g..4g+3.
+  // Lane (sub, h) holds row m = 32jb + sub, columns n0 + 32w + 8g + 4h + (0..3) in registers 4g..4g+3: block
+  // (jb, n0 / 32 + w) of this chunk's plane, written whole (partial_block_offset's layout).
   int32_t* out = acc + blockIdx.y * plane;
+  const int nbn = (N + 31) / 32, bn = n0 / 32 + wave;
+  if (32 * bn >= N) return;
 #pragma unroll
   for (int jb = 0; jb < 2; ++jb) {
-    const int m = jb * 32 + sub;
-    if (m >= M) continue;
+    if (32 * jb >= M) continue;
+    v4i* dst = reinterpret_cast<v4i*>(out + partial_block_offset(jb, bn, nbn) + 4 * lane);
+    const v16i& c = acc_r[jb];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int n = n0 + wave * 32 + 8 * g + 4 * half;
-      int32_t* dst = out + (int64_t)m * ld_acc + n;
-      const v16i& c = acc_r[jb];
-      if (n + 4 <= N) {
-        *reinterpret_cast<v4i*>(dst) = (v4i){c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
-      } else {
-        for (int e = 0; e < 4; ++e)
-          if (n + e < N) dst[e] = c[4 * g + e];
-      }
-    }
+    for (int g = 0; g < 4; ++g) dst[64 * g] = (v4i){c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
   }
 }
+
+template __global__ void skinny_gemm_kernel<false>(const int8_t*, int64_t, const int8_t*, int64_t, int32_t*, int64_t,
+                                                   int, int, int, int, int, int);
+template __global__ void skinny_gemm_kernel<true>(const int8_t*, int64_t, const int8_t*, int64_t, int32_t*, int64_t,
+                                                  int, int, int, int, int, int);
 
 }  // namespace hf

@@ -5,9 +5,9 @@
 // reference's (src/hyperflow_h3_flash/int8.py:179), as from the unsplit GEMM. `act` applies the same output activation
 // as the GEMM's epilogue (kActNone, kActGeluTanh, or kActSwiGLU).
 //
-// kActSwiGLU: the partials hold the N columns in the weight's natural order; the epilogue walks them in pair order
-// (logical column n reads accumulator column, wscale, bias and up row glu_row(n)), so in each 32-column tile register
-// v < 8 holds a hidden column and v + 8 its gate column, and the tile writes 16 of the N / 2 outputs.
+// The planes are stored block by block (partial_block_offset): wave (bm, bn) reads block (bm, bn) of each. kActSwiGLU: the GEMMs that wrote the partials read the weight rows in pair order (column n is weight row
+// glu_row(n)), so the epilogue reads wscale, bias and up row glu_row(n) for column n; in each 32-column block register
+// v < 8 holds a hidden column and v + 8 its gate column, and the block writes 16 of the N / 2 outputs.
 //
 // With few rows (M <= a few hundred) the unsplit GEMM has fewer 256 x 256 tiles than the chip has CUs; splitting K
 // gives every CU a share of the weight stream, at the cost of writing and re-reading M x N int32 per split.
@@ -21,9 +21,8 @@ namespace hf {
 
 constexpr int kSkTileM = 32;
 constexpr int kSkTileN = 32;
-constexpr int kSkMaxSplits = 32;
 
-__global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __restrict__ acc, int64_t ld_acc,
+__global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __restrict__ acc,
                                                              int64_t plane, int splits, const float* __restrict__ sx,
                                                              const float* __restrict__ sw,
                                                              const uint16_t* __restrict__ u, int64_t ldu,
@@ -40,33 +39,37 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
   const int m0 = (blockIdx.x / tiles_n) * kSkTileM, n0 = (blockIdx.x % tiles_n) * kSkTileN;
   const int m = m0 + sub;
   const float sxm = sx[min(m, M - 1)];
+  // The planes' sums at this lane's 16 positions in block (bm, bn) of each plane (partial_block_offset's layout:
+  // each of the wave's loads covers 1 KiB of contiguous memory). Loads are issued eight planes at a time before any
+  // is added; the sums are exact in any order.
+  int32_t sums[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sums[i] = 0;
+  const int32_t* blk = acc + partial_block_offset(m0 / 32, n0 / 32, tiles_n) + 4 * lane;
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    v4i pl[8][4];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        pl[s][gq] =
+            (s0 + s < splits) ? reinterpret_cast<const v4i*>(blk + (int64_t)(s0 + s) * plane)[64 * gq] : (v4i){0};
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sums[4 * gq + e] += pl[s][gq][e];
+  }
   v16f c;
 #pragma unroll
   for (int gq = 0; gq < 4; ++gq) {
     const int n = n0 + 8 * gq + 4 * half;
     const int na = (n < N) ? col(n) : n;
-    int32_t s4[4] = {0, 0, 0, 0};
-    if (m < M) {
-      if (vec && n + 4 <= N) {
-        // Every plane's four values are loaded before any is added (splits <= kSkMaxSplits); the sum is exact.
-        v4i pl[kSkMaxSplits];
-#pragma unroll
-        for (int s = 0; s < kSkMaxSplits; ++s)
-          pl[s] = s < splits ? *reinterpret_cast<const v4i*>(acc + s * plane + (int64_t)m * ld_acc + na) : (v4i){0};
-#pragma unroll
-        for (int s = 0; s < kSkMaxSplits; ++s)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) s4[e] += pl[s][e];
-      } else {
-        for (int s = 0; s < splits; ++s)
-          for (int e = 0; e < 4; ++e)
-            if (n + e < N) s4[e] += acc[s * plane + (int64_t)m * ld_acc + na + e];
-      }
-    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float wsn = (n + e < N) ? sw[na + e] : 0.0f;
-      c[4 * gq + e] = ((float)s4[e] * sxm) * wsn;
+      c[4 * gq + e] = ((float)sums[4 * gq + e] * sxm) * wsn;
     }
   }
   // Low-rank term, 16 ranks per MFMA: first operand up[n, :], second u[m, :] (rows past the matrix read zero).
