@@ -341,6 +341,8 @@ void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
+    // A tile wholly past K (the last wave of a row whose tiles do not split evenly) costs no rotation work.
+    if ((t0 + i) * kRqTile >= kvalid) continue;
     const uint4 a = make_uint4(held[i][0], held[i][1], held[i][2], held[i][3]);
     const uint4 b = make_uint4(held[i][4], held[i][5], held[i][6], held[i][7]);
     amax = fmaxf(amax, rotate_tile_packed<LOG4G>(a, b, lane, scratch, held[i]));
