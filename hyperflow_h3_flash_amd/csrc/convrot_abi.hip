@@ -65,10 +65,12 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<4>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<1>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLrLds);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<2>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLrLds);
+#define HF_LR_ATTR(RB, NW)                                                                                \
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<RB, NW>),             \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::lr_lds(NW));
+    HF_LR_ATTR(1, 4) HF_LR_ATTR(1, 5) HF_LR_ATTR(1, 6) HF_LR_ATTR(1, 7) HF_LR_ATTR(1, 8)
+    HF_LR_ATTR(2, 4) HF_LR_ATTR(2, 5) HF_LR_ATTR(2, 6) HF_LR_ATTR(2, 7) HF_LR_ATTR(2, 8)
+#undef HF_LR_ATTR
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_up_kernel),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kUpLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel<false>),
@@ -193,10 +195,10 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
   if (K % 16 || !aligned(x, 16) || !aligned(down, 16) || (ldx % 8) || (ld_down % 8) || !aligned(u, 8))
     return HF_ERR_ALIGNMENT;
   if (M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HF_ERR_SIZE;
-  if (2 * hf::kLrRows * ldx >= (int64_t(1) << 31) || 2 * hf::kLrRanks * ld_down >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  if (2 * hf::kLrMaxRows * ldx >= (int64_t(1) << 31) || 2 * hf::kLrRanks * ld_down >= (int64_t(1) << 31))
+    return HF_ERR_SIZE;
   allow_large_lds();
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const unsigned blocks = (unsigned)((M + hf::kLrRows - 1) / hf::kLrRows);
   LrPlan plan = lowrank_plan(M, K);
   if (plan.splits > 1 && (!ws || ws_bytes < (int64_t)plan.splits * M * std::min<int32_t>(r, hf::kLrRanks) * 4 ||
                           !aligned(ws, 16))) {
@@ -204,18 +206,30 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
     plan.k_chunk = (int)K;
   }
   float* part = plan.splits > 1 ? static_cast<float*>(ws) : nullptr;
+  // Waves per workgroup (32 rows each): the fewest that cover the rows in one round of one workgroup per CU, from 4
+  // (128 rows) to 8; split launches keep 4.
+  int nw = 4;
+  if (plan.splits == 1) {
+    const int64_t per_cu = (M + device_cus() - 1) / device_cus();
+    nw = (int)std::min<int64_t>(std::max<int64_t>((per_cu + 31) / 32, 4), hf::kLrMaxWaves);
+  }
+  const unsigned blocks = (unsigned)((M + 32 * nw - 1) / (32 * nw));
   for (int32_t j0 = 0; j0 < r; j0 += hf::kLrRanks) {
     const int rr = std::min<int32_t>(hf::kLrRanks, r - j0);
     const uint16_t* d = down + (int64_t)j0 * ld_down;
     uint16_t* uo = u + j0;
-    const dim3 grid(blocks, (unsigned)plan.splits);
-    if (rr <= 32) {
-      hipLaunchKernelGGL(hf::lowrank_down_kernel<1>, grid, dim3(hf::kLrThreads), hf::kLrLds, s, x, ldx, d, ld_down, uo,
-                         ldu, (int)M, (int)K, rr, plan.k_chunk, part);
-    } else {
-      hipLaunchKernelGGL(hf::lowrank_down_kernel<2>, grid, dim3(hf::kLrThreads), hf::kLrLds, s, x, ldx, d, ld_down, uo,
-                         ldu, (int)M, (int)K, rr, plan.k_chunk, part);
-    }
+    const dim3 grid(blocks, (unsigned)plan.splits), block(64 * nw);
+#define HF_LR_CASE(NW)                                                                                              \
+  if (nw == NW) {                                                                                                   \
+    if (rr <= 32)                                                                                                   \
+      hipLaunchKernelGGL((hf::lowrank_down_kernel<1, NW>), grid, block, hf::lr_lds(NW), s, x, ldx, d, ld_down, uo,  \
+                         ldu, (int)M, (int)K, rr, plan.k_chunk, part);                                              \
+    else                                                                                                            \
+      hipLaunchKernelGGL((hf::lowrank_down_kernel<2, NW>), grid, block, hf::lr_lds(NW), s, x, ldx, d, ld_down, uo,  \
+                         ldu, (int)M, (int)K, rr, plan.k_chunk, part);                                              \
+  }
+    HF_LR_CASE(4) HF_LR_CASE(5) HF_LR_CASE(6) HF_LR_CASE(7) HF_LR_CASE(8)
+#undef HF_LR_CASE
     int st = launch_status();
     if (st != HF_OK) return st;
     if (part) {

@@ -13,15 +13,24 @@
 
 namespace hf {
 
-constexpr int kLrRows = 128;                          // x rows per workgroup
+// A workgroup of NW waves (4..8) owns 32 NW x rows. The host picks NW so one round of workgroups covers the rows
+// when it can (at most one workgroup per CU fits): 4 waves up to 256 CUs x 128 rows, more for a few more rows (the
+// 5.2 s clip's 37710 tokens take 236 workgroups of 160 rows instead of 295 of 128, whose last 39 would run alone).
+constexpr int kLrRows = 128;                          // x rows per workgroup with 4 waves (the split-K launches)
+constexpr int kLrMaxWaves = 8;
+constexpr int kLrMaxRows = 32 * kLrMaxWaves;
 constexpr int kLrRanks = 64;                          // ranks per launch
 constexpr int kLrStageK = 64;                         // K elements per stage (128-byte row segments)
-constexpr int kLrXBytes = kLrRows * kLrStageK * 2;    // 16 KiB
-constexpr int kLrDBytes = kLrRanks * kLrStageK * 2;   // 8 KiB
-constexpr int kLrStageBytes = kLrXBytes + kLrDBytes;  // 24 KiB
-constexpr int kLrStages = 6;
-constexpr int kLrLds = kLrStages * kLrStageBytes;     // 144 KiB
-constexpr int kLrThreads = 256;
+constexpr int kLrDBytes = kLrRanks * kLrStageK * 2;   // 8 KiB of down per stage
+constexpr int kLrThreads = 256;                       // with 4 waves
+
+__host__ __device__ constexpr int lr_stage_bytes(int nw) { return nw * 32 * kLrStageK * 2 + kLrDBytes; }
+// Ring depth: as many stages as fit 160 KiB, at most 6 (6 stages of 24 KiB with 4 waves).
+__host__ __device__ constexpr int lr_stages(int nw) {
+  return (160 * 1024) / lr_stage_bytes(nw) < 6 ? (160 * 1024) / lr_stage_bytes(nw) : 6;
+}
+__host__ __device__ constexpr int lr_lds(int nw) { return lr_stages(nw) * lr_stage_bytes(nw); }
+constexpr int kLrLds = lr_lds(4);                     // 144 KiB
 
 // LDS rows are 128 bytes (eight 16-byte chunks), swizzled with swizzle128 so fragment reads are conflict-free.
 __device__ __forceinline__ int lr_swizzle(int row, int c) { return swizzle128(row, c); }
@@ -45,19 +54,24 @@ __device__ __forceinline__ void lr_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t oo
 // Split K (few rows): blockIdx.y = s covers K elements [s * k_chunk, (s + 1) * k_chunk) and writes its fp32 partial
 // sums to plane s of `part` ([splits][M][r]); lowrank_reduce_kernel adds the planes and rounds to bf16. Unsplit
 // launches (gridDim.y == 1, part == nullptr) write u directly.
-template <int RB>
-__global__ __launch_bounds__(kLrThreads, 1) void lowrank_down_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                                     const uint16_t* __restrict__ down, int64_t ldd,
-                                                                     uint16_t* __restrict__ u, int64_t ldu, int M,
-                                                                     int K, int r, int k_chunk,
-                                                                     float* __restrict__ part) {
+template <int RB, int NW = 4>
+__global__ __launch_bounds__(64 * NW, 1) void lowrank_down_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                  const uint16_t* __restrict__ down, int64_t ldd,
+                                                                  uint16_t* __restrict__ u, int64_t ldu, int M,
+                                                                  int K, int r, int k_chunk,
+                                                                  float* __restrict__ part) {
+  constexpr int kRows = 32 * NW;
+  constexpr int kXBytes = kRows * kLrStageK * 2;
+  constexpr int kStageBytes = lr_stage_bytes(NW);
+  constexpr int kStages = lr_stages(NW);
+  static_assert(kStages >= 4 && kStages <= 6, "ring depth");
   extern __shared__ __attribute__((aligned(1024))) unsigned char lr_smem_raw[];
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)lr_smem_raw;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane & 31, half = lane >> 5;
-  const int m0 = blockIdx.x * kLrRows;
-  const int rows_m = min(kLrRows, M - m0);
+  const int m0 = blockIdx.x * kRows;
+  const int rows_m = min(kRows, M - m0);
 
   const int k_lo = blockIdx.y * k_chunk;
   const int k_len = min(K - k_lo, k_chunk);
@@ -66,12 +80,14 @@ __global__ __launch_bounds__(kLrThreads, 1) void lowrank_down_kernel(const uint1
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (int64_t)m0 * ldx + k_lo, bytes_x - 2u * (uint32_t)k_lo);
   const __amdgpu_buffer_rsrc_t rd = make_rsrc(down + k_lo, bytes_d - 2u * (uint32_t)k_lo);
 
-  // Stage t -> slot t % kLrStages; every stage issues 6 loads per wave (4 of x, 2 of down), stages past the end
-  // load zeros, so "stage t has landed" is always vmcnt(24) with the four later stages in flight.
+  // Stage t -> slot t % kStages; every stage issues 6 loads per wave (4 of its 32 x rows, 2 of the 8 blocks of
+  // down: waves past the fourth load the first waves' blocks again, the same bytes to the same place, so every wave
+  // issues the same count), stages past the end load zeros, so "stage t has landed" is always a constant vmcnt with
+  // the kStages - 2 later stages in flight.
   auto issue = [&](int t) {
-    unsigned char HF_LDS* st = smem + (t % kLrStages) * kLrStageBytes;
+    unsigned char HF_LDS* st = smem + (t % kStages) * kStageBytes;
     lr_load<4>(rx, bytes_x, ldx_bytes, rows_m, t * kLrStageK, k_len, st, wave * 4, lane);
-    lr_load<2>(rd, bytes_d, ldd_bytes, r, t * kLrStageK, k_len, st + kLrXBytes, wave * 2, lane);
+    lr_load<2>(rd, bytes_d, ldd_bytes, r, t * kLrStageK, k_len, st + kXBytes, (wave % 4) * 2, lane);
   };
 
   v16f acc[RB];
@@ -80,14 +96,20 @@ __global__ __launch_bounds__(kLrThreads, 1) void lowrank_down_kernel(const uint1
 
   const int nst = (k_len + kLrStageK - 1) / kLrStageK;
 #pragma unroll
-  for (int t = 0; t < kLrStages - 1; ++t) issue(t);
+  for (int t = 0; t < kStages - 1; ++t) issue(t);
   const int xrow = wave * 32 + sub;
   for (int t = 0; t < nst; ++t) {
-    // This wave's loads of stage t have landed and its reads of slot (t - 1) % 6 have returned; the barrier (no
-    // memory fence, which would also wait for the four stages behind) makes that true for every wave.
-    asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    issue(t + kLrStages - 1);
-    const unsigned char HF_LDS* st = smem + (t % kLrStages) * kLrStageBytes;
+    // This wave's loads of stage t have landed and its reads of slot (t - 1) % kStages have returned; the barrier (no
+    // memory fence, which would also wait for the stages behind) makes that true for every wave.
+    if constexpr (kStages == 6) {
+      asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else if constexpr (kStages == 5) {
+      asm volatile("s_waitcnt vmcnt(18) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    issue(t + kStages - 1);
+    const unsigned char HF_LDS* st = smem + (t % kStages) * kStageBytes;
 #pragma unroll
     for (int s = 0; s < kLrStageK / 16; ++s) {
       const int c = 2 * s + half;
@@ -96,7 +118,7 @@ __global__ __launch_bounds__(kLrThreads, 1) void lowrank_down_kernel(const uint1
       for (int rb = 0; rb < RB; ++rb) {
         const int drow = rb * 32 + sub;
         const v8bf df =
-            *reinterpret_cast<const v8bf HF_LDS*>(st + kLrXBytes + drow * 128 + lr_swizzle(drow, c) * 16);
+            *reinterpret_cast<const v8bf HF_LDS*>(st + kXBytes + drow * 128 + lr_swizzle(drow, c) * 16);
         acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(df, xf, acc[rb], 0, 0, 0);
       }
     }
@@ -135,10 +157,12 @@ __global__ __launch_bounds__(kLrThreads, 1) void lowrank_down_kernel(const uint1
   }
 }
 
-template __global__ void lowrank_down_kernel<1>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
-                                                int64_t, int, int, int, int, float*);
-template __global__ void lowrank_down_kernel<2>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
-                                                int64_t, int, int, int, int, float*);
+#define HF_LR_DOWN(RB, NW)                                                                                          \
+  template __global__ void lowrank_down_kernel<RB, NW>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*, \
+                                                       int64_t, int, int, int, int, float*);
+HF_LR_DOWN(1, 4) HF_LR_DOWN(1, 5) HF_LR_DOWN(1, 6) HF_LR_DOWN(1, 7) HF_LR_DOWN(1, 8)
+HF_LR_DOWN(2, 4) HF_LR_DOWN(2, 5) HF_LR_DOWN(2, 6) HF_LR_DOWN(2, 7) HF_LR_DOWN(2, 8)
+#undef HF_LR_DOWN
 
 constexpr int kMaxSplits = 32;  // K chunks of a split launch, at most
 

@@ -267,6 +267,26 @@ def test_lowrank_down_matches_oracle(oracle_lib, rank):
     assert (got == ref).mean() > 0.99
 
 
+@pytest.mark.parametrize("m,rank", [(32768, 64), (37710, 64), (45000, 32), (60001, 64), (70000, 136)])
+def test_lowrank_down_many_rows_on_sampled_rows(oracle_lib, m, rank):
+    """Row counts that take 4 to 8 waves per workgroup (one round of workgroups up to 256 x 256 rows, more rounds
+    past it), a ragged last workgroup and a rank split over two launches; the oracle checks a seeded sample of rows
+    and the last rows."""
+    from hyperflow_h3_flash_amd.int8 import lowrank_down
+
+    k = 1024
+    gen = torch.Generator(device=DEV).manual_seed(m + rank)
+    x = torch.randn(m, k, device=DEV, generator=gen).to(torch.bfloat16)
+    down = (torch.randn(rank, k, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    u = lowrank_down(x, down)
+    torch.cuda.synchronize()
+    rows = np.concatenate([np.sort(np.random.default_rng(m).choice(m, size=24, replace=False)), np.arange(m - 8, m)])
+    got = oracle_lib.bf16_to_f32(bits_of(u[rows]))
+    ref = oracle_lib.bf16_to_f32(oracle_lib.lowrank_down(bits_of(x[rows]), bits_of(down)))
+    assert (np.abs(got - ref) <= np.abs(ref) * 2.0**-7 + 1e-7).all()
+    assert (got == ref).mean() > 0.99
+
+
 # ------------------------------------------------------------------------------------------- benchmark-size shapes
 
 
