@@ -174,21 +174,36 @@ __device__ __forceinline__ RowScale row_scale(float amax) {
 }
 
 // Quantizes 8 packed bf16 pairs (int8.py:178): value v = 2i + h of the pairs becomes byte v % 4 of out[v / 4].
-__device__ __forceinline__ void quantize_packed(const uint32_t (&w)[8], const RowScale& rs, uint32_t (&out)[4]) {
+// The quotient of a value by the row's scale is at most 127 in magnitude (the absmax maps to 127 and nothing is
+// larger), so the reference's clamp never acts on finite input. Rounding to an integer is an add of 1.5 * 2^23: the
+// sum's exponent leaves units in the last place, so the add rounds the quotient to an integer, ties to even (torch's
+// round), and the integer's two's-complement low byte is the sum's low byte; v_perm_b32 gathers four such bytes.
+// (Non-finite input gives unspecified codes, as the reference's int8 cast of NaN does.)
+// The 16 codes of 8 packed bf16 pairs, each in the low byte of its word (value v = 2i + h of the pairs in word v).
+__device__ __forceinline__ void quantize_bytes(const uint32_t (&w)[8], const RowScale& rs, uint32_t (&b)[16]) {
+  constexpr float kRoundMagic = 12582912.0f;  // 1.5 * 2^23
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    b[2 * i] = __float_as_uint(quotient(bf16_lo(w[i]), rs.d, rs.inv) + kRoundMagic);
+    b[2 * i + 1] = __float_as_uint(quotient(bf16_hi(w[i]), rs.d, rs.inv) + kRoundMagic);
+  }
+}
+
+// The low bytes of 16 words packed into 4 (word v's byte becomes byte v % 4 of out[v / 4]).
+__device__ __forceinline__ void pack_low_bytes(const uint32_t (&b)[16], uint32_t (&out)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t pair = w[2 * i + h];
-      float r0 = rintf(quotient(bf16_lo(pair), rs.d, rs.inv));
-      float r1 = rintf(quotient(bf16_hi(pair), rs.d, rs.inv));
-      r0 = fminf(fmaxf(r0, -127.0f), 127.0f);
-      r1 = fminf(fmaxf(r1, -127.0f), 127.0f);
-      word |= ((uint32_t)((int)r0 & 0xff) | ((uint32_t)((int)r1 & 0xff) << 8)) << (16 * h);
-    }
-    out[i] = word;
+    // perm(a, b, sel): selector byte k picks byte k of b (0-3) or of a (4-7); 0x0c gives zero.
+    const uint32_t lo = __builtin_amdgcn_perm(b[4 * i + 1], b[4 * i], 0x0c0c0400u);      // bytes: v0, v1, 0, 0
+    const uint32_t hi = __builtin_amdgcn_perm(b[4 * i + 3], b[4 * i + 2], 0x04000c0cu);  // bytes: 0, 0, v2, v3
+    out[i] = lo | hi;
   }
+}
+
+__device__ __forceinline__ void quantize_packed(const uint32_t (&w)[8], const RowScale& rs, uint32_t (&out)[4]) {
+  uint32_t b[16];
+  quantize_bytes(w, rs, b);
+  pack_low_bytes(b, out);
 }
 
 // Quantizes this lane's 16 elements of tile t from the row buffer (int8.py:178) and writes them (16 bytes).
@@ -284,21 +299,26 @@ __global__ __launch_bounds__(1024) void rotate_quant_row_kernel(const uint16_t* 
 // row combine their absmax through LDS, then each quantizes its own tiles; the bytes of a tile go back to natural
 // order through the (now free) transpose area so every lane stores 16 consecutive bytes. Same arithmetic as
 // rotate_quant_kernel.
+// Writes a tile's 16 codes per lane (each in the low byte of its word, in the layout of held_offset) to the row in
+// natural order: directly for LOG4G <= 2, else through the wave's staging bytes (each code written straight from
+// its word, then 16 consecutive bytes read back per lane).
 template <int LOG4G>
-__device__ __forceinline__ void store_quantized_tile(const uint32_t (&out)[4], int base, int K, int lane,
-                                                     unsigned char* stage, int8_t* qrow) {
+__device__ __forceinline__ void store_codes(const uint32_t (&b)[16], int base, int K, int lane, unsigned char* stage,
+                                            int8_t* qrow) {
   if constexpr (LOG4G <= 2) {
+    uint32_t out[4];
+    pack_low_bytes(b, out);
     if (base + lane * 16 < K)
       *reinterpret_cast<uint4*>(qrow + base + lane * 16) = make_uint4(out[0], out[1], out[2], out[3]);
   } else {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint32_t two = (out[j >> 1] >> (16 * (j & 1))) & 0xffffu;  // values 2j, 2j + 1
       if constexpr (LOG4G == 3) {
-        *reinterpret_cast<uint16_t*>(stage + held_offset<LOG4G>(lane, j, 0)) = (uint16_t)two;
+        *reinterpret_cast<uint16_t*>(stage + held_offset<LOG4G>(lane, j, 0)) =
+            (uint16_t)__builtin_amdgcn_perm(b[2 * j + 1], b[2 * j], 0x0c0c0400u);
       } else {
-        stage[held_offset<LOG4G>(lane, j, 0)] = (unsigned char)two;
-        stage[held_offset<LOG4G>(lane, j, 1)] = (unsigned char)(two >> 8);
+        stage[held_offset<LOG4G>(lane, j, 0)] = (unsigned char)b[2 * j];
+        stage[held_offset<LOG4G>(lane, j, 1)] = (unsigned char)b[2 * j + 1];
       }
     }
     wave_lds_sync();
@@ -306,6 +326,15 @@ __device__ __forceinline__ void store_quantized_tile(const uint32_t (&out)[4], i
       *reinterpret_cast<uint4*>(qrow + base + lane * 16) = *reinterpret_cast<const uint4*>(stage + lane * 16);
     wave_lds_sync();  // the next tile rewrites the staging bytes
   }
+}
+
+// Quantizes one held tile (8 packed bf16 pairs in the layout of held_offset) and writes its codes (store_codes).
+template <int LOG4G>
+__device__ __forceinline__ void quantize_store_tile(const uint32_t (&w)[8], const RowScale& rs, int base, int K,
+                                                    int lane, unsigned char* stage, int8_t* qrow) {
+  uint32_t b[16];
+  quantize_bytes(w, rs, b);
+  store_codes<LOG4G>(b, base, K, lane, stage, qrow);
 }
 
 size_t rotate_quant_reg_lds_bytes(int waves) { return (size_t)waves * kRqScratchBytes + 16; }
@@ -360,11 +389,7 @@ void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     const int base = (t0 + i) * kRqTile;
-    if (base < K) {
-      uint32_t out[4];
-      quantize_packed(held[i], rs, out);
-      store_quantized_tile<LOG4G>(out, base, K, lane, stage, qrow);
-    }
+    if (base < K) quantize_store_tile<LOG4G>(held[i], rs, base, K, lane, stage, qrow);
   }
 }
 
@@ -405,18 +430,12 @@ __global__ __launch_bounds__(256) void rotate_quant_f32_recip_kernel(const uint1
       load_pencil(xrow, t * kRqTile + lane * 16, K, a, b);
       double v[16];
       rotate_tile_f64<LOG4G>(a, b, lane, scratch, v);
-      uint32_t out[4];
+      // |xr * inv| <= 127 (the absmax maps to 127): the clamp never acts on finite input; the rounding add of
+      // quantize_bytes gives rint and the code in the low byte.
+      uint32_t codes[16];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float r = fminf(fmaxf(rintf((float)v[4 * i + j] * inv_n), -127.0f), 127.0f);
-          word |= ((uint32_t)((int)r & 0xff)) << (8 * j);
-        }
-        out[i] = word;
-      }
-      store_quantized_tile<LOG4G>(out, t * kRqTile, K, lane, stage, qrow);
+      for (int i = 0; i < 16; ++i) codes[i] = __float_as_uint((float)v[i] * inv_n + 12582912.0f);
+      store_codes<LOG4G>(codes, t * kRqTile, K, lane, stage, qrow);
     }
   }
 }
