@@ -23,7 +23,7 @@ namespace hf {
 constexpr int kRqTile = 1024;                            // elements per wave step (64 lanes x 16)
 constexpr int kRqStride = 18;                            // doubles per pencil in the transpose scratch (16 + pad)
 constexpr int kRqScratchBytes = 64 * kRqStride * 8;      // 9216 bytes per wave
-constexpr int kRqRegMaxTpw = 5;  // tiles per wave of the register-resident kernel (held in at most 128 VGPRs)
+constexpr int kRqRegMaxTpw = 5;  // tiles per wave of the register-resident kernel (three waves per SIMD at five)
 
 __device__ __forceinline__ void h4(double& a, double& b, double& c, double& d) {
   double s = (a + b) + (c + d);
@@ -127,6 +127,22 @@ __device__ __forceinline__ float rotate_tile_packed(uint4 cur0, uint4 cur1, int 
   return amax;
 }
 
+// rotate_tile_f64, then every value rounded once to bf16, returned as fp32 values (the layout of held_offset), with
+// this lane's absmax of the rounded, still unnormalised sums.
+template <int LOG4G>
+__device__ __forceinline__ float rotate_tile_rounded(uint4 cur0, uint4 cur1, int lane, double* scratch,
+                                                     float (&f)[16]) {
+  float amax = 0.0f;
+  double v[16];
+  rotate_tile_f64<LOG4G>(cur0, cur1, lane, scratch, v);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    f[i] = round_f64_to_bf16_value(v[i]);
+    amax = fmaxf(amax, fabsf(f[i]));
+  }
+  return amax;
+}
+
 // Rotates tile t of a row and parks the rounded bf16 bits in `rowbuf` (the row's buffer) at their natural positions
 // (elements at or past K are not written). Returns this lane's absmax.
 template <int LOG4G>
@@ -179,14 +195,21 @@ __device__ __forceinline__ RowScale row_scale(float amax) {
 // sum's exponent leaves units in the last place, so the add rounds the quotient to an integer, ties to even (torch's
 // round), and the integer's two's-complement low byte is the sum's low byte; v_perm_b32 gathers four such bytes.
 // (Non-finite input gives unspecified codes, as the reference's int8 cast of NaN does.)
+constexpr float kRoundMagic = 12582912.0f;  // 1.5 * 2^23
+
 // The 16 codes of 8 packed bf16 pairs, each in the low byte of its word (value v = 2i + h of the pairs in word v).
 __device__ __forceinline__ void quantize_bytes(const uint32_t (&w)[8], const RowScale& rs, uint32_t (&b)[16]) {
-  constexpr float kRoundMagic = 12582912.0f;  // 1.5 * 2^23
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     b[2 * i] = __float_as_uint(quotient(bf16_lo(w[i]), rs.d, rs.inv) + kRoundMagic);
     b[2 * i + 1] = __float_as_uint(quotient(bf16_hi(w[i]), rs.d, rs.inv) + kRoundMagic);
   }
+}
+
+// The same for 16 values held as fp32 (each exactly a bf16 value).
+__device__ __forceinline__ void quantize_values(const float (&f)[16], const RowScale& rs, uint32_t (&b)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) b[i] = __float_as_uint(quotient(f[i], rs.d, rs.inv) + kRoundMagic);
 }
 
 // The low bytes of 16 words packed into 4 (word v's byte becomes byte v % 4 of out[v / 4]).
@@ -292,13 +315,12 @@ __global__ __launch_bounds__(1024) void rotate_quant_row_kernel(const uint16_t* 
   quantize_tile(rowbuf, t, K, lane, rs, q + row * ldq);  // this wave's own tile: its writes are visible to it
 }
 
-// Many rows, rows up to 20 tiles: the rounded row stays in registers instead of an LDS row buffer, so a workgroup
-// needs only the fp64 transpose areas and occupancy is set by registers (3 waves per SIMD at 5 tiles per wave). A
-// row is split over `wpr` waves of TPW <= 5 consecutive tiles each; a workgroup holds 4 / wpr rows (one when
-// wpr = 3). The waves of a
-// row combine their absmax through LDS, then each quantizes its own tiles; the bytes of a tile go back to natural
-// order through the (now free) transpose area so every lane stores 16 consecutive bytes. Same arithmetic as
-// rotate_quant_kernel.
+// Many rows, rows up to 20 tiles: the rounded row stays in registers (as fp32) instead of an LDS row buffer, so a
+// workgroup needs only the fp64 transpose areas and occupancy is set by registers (3 waves per SIMD at 5 tiles per
+// wave). A row is split over `wpr` waves of TPW <= 5 consecutive tiles each; a workgroup holds 4 / wpr rows (one when
+// wpr = 3). The waves of a row combine their absmax through LDS, then each quantizes its own tiles; the bytes of a
+// tile go back to natural order through the (now free) transpose area so every lane stores 16 consecutive bytes.
+// Same arithmetic as rotate_quant_kernel.
 // Writes a tile's 16 codes per lane (each in the low byte of its word, in the layout of held_offset) to the row in
 // natural order: directly for LOG4G <= 2, else through the wave's staging bytes (each code written straight from
 // its word, then 16 consecutive bytes read back per lane).
@@ -328,20 +350,21 @@ __device__ __forceinline__ void store_codes(const uint32_t (&b)[16], int base, i
   }
 }
 
-// Quantizes one held tile (8 packed bf16 pairs in the layout of held_offset) and writes its codes (store_codes).
+// Quantizes one held tile (16 fp32 values in the layout of held_offset) and writes its codes (store_codes).
 template <int LOG4G>
-__device__ __forceinline__ void quantize_store_tile(const uint32_t (&w)[8], const RowScale& rs, int base, int K,
+__device__ __forceinline__ void quantize_store_tile(const float (&f)[16], const RowScale& rs, int base, int K,
                                                     int lane, unsigned char* stage, int8_t* qrow) {
   uint32_t b[16];
-  quantize_bytes(w, rs, b);
+  quantize_values(f, rs, b);
   store_codes<LOG4G>(b, base, K, lane, stage, qrow);
 }
 
 size_t rotate_quant_reg_lds_bytes(int waves) { return (size_t)waves * kRqScratchBytes + 16; }
 
-// Five tiles per wave fit 128 VGPRs (four waves per SIMD) when the compiler is held to it.
+// Five tiles per wave held as fp32 (80 VGPRs; ~136 in all) leave three waves per SIMD when the compiler is held to
+// it. Holding them as packed bf16 pairs (four waves per SIMD) cost a pack and an unpack per value: 3-5 % slower.
 template <int LOG4G, int TPW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TPW == kRqRegMaxTpw ? 4 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TPW == kRqRegMaxTpw ? 3 : 1)))
 void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
                              float* __restrict__ s, int64_t M, int K, int wpr) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -357,24 +380,27 @@ void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t
   const uint16_t* xrow = x + (live ? row : 0) * ldx;
   const int t0 = part * TPW;
 
-  // held[i] first receives tile i's raw pencil (all of this wave's loads in flight at once), then its rounded
-  // values.
-  uint32_t held[TPW][8];
+  // held[i] first receives tile i's raw pencil in its first 8 words (all of this wave's loads in flight at once),
+  // then the tile's 16 rounded values.
+  float held[TPW][16];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     uint4 a, b;
     load_pencil(xrow, (t0 + i) * kRqTile + lane * 16, kvalid, a, b);
-    held[i][0] = a.x; held[i][1] = a.y; held[i][2] = a.z; held[i][3] = a.w;
-    held[i][4] = b.x; held[i][5] = b.y; held[i][6] = b.z; held[i][7] = b.w;
+    const uint32_t raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) held[i][j] = __uint_as_float(raw[j]);
   }
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
     // A tile wholly past K (the last wave of a row whose tiles do not split evenly) costs no rotation work.
     if ((t0 + i) * kRqTile >= kvalid) continue;
-    const uint4 a = make_uint4(held[i][0], held[i][1], held[i][2], held[i][3]);
-    const uint4 b = make_uint4(held[i][4], held[i][5], held[i][6], held[i][7]);
-    amax = fmaxf(amax, rotate_tile_packed<LOG4G>(a, b, lane, scratch, held[i]));
+    const uint4 a = make_uint4(__float_as_uint(held[i][0]), __float_as_uint(held[i][1]), __float_as_uint(held[i][2]),
+                               __float_as_uint(held[i][3]));
+    const uint4 b = make_uint4(__float_as_uint(held[i][4]), __float_as_uint(held[i][5]), __float_as_uint(held[i][6]),
+                               __float_as_uint(held[i][7]));
+    amax = fmaxf(amax, rotate_tile_rounded<LOG4G>(a, b, lane, scratch, held[i]));
   }
   amax = wave_max(amax);
   if (lane == 0) maxes[wave] = amax;
@@ -434,7 +460,7 @@ __global__ __launch_bounds__(256) void rotate_quant_f32_recip_kernel(const uint1
       // quantize_bytes gives rint and the code in the low byte.
       uint32_t codes[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) codes[i] = __float_as_uint((float)v[i] * inv_n + 12582912.0f);
+      for (int i = 0; i < 16; ++i) codes[i] = __float_as_uint((float)v[i] * inv_n + kRoundMagic);
       store_codes<LOG4G>(codes, t * kRqTile, K, lane, stage, qrow);
     }
   }
