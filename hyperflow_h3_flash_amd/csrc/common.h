@@ -90,16 +90,16 @@ __device__ __forceinline__ uint32_t activate_bf16x2(uint32_t pair) {
   return pair;
 }
 
-// Rounds an fp64 value to 8 significant bits (bf16 precision) with round-to-nearest-even, once, directly from the
-// fp64 bits: the kept bits end at bit 13 of the high word; bit 12 is the rounding bit and bits 11..0 of the high
-// word plus the whole low word are sticky. Adding 0xFFF + (lsb | sticky_low) carries into bit 13 exactly when RNE
-// rounds up. The result has at most 8 significant bits, so the fp32 conversion is exact (inf beyond fp32 range).
+// Rounds an fp64 value to 8 significant bits (bf16 precision) with round-to-nearest-even, once, and returns it as
+// fp32 (exact: 8 significant bits; inf beyond the fp32 range). Adding c = +-2^(e + 45) (the value's sign and binade
+// e, from its high word) leaves the sum in binade e + 45, whose unit in the last place is 2^(e - 7), so the fp64 add
+// rounds the value to 8 significant bits, ties to even; subtracting c again is exact. A zero input gives +0 (c is a
+// tiny normal number). Two fp64 adds and two integer operations in place of the bit-level rounding (sticky bit,
+// carry, mask: five), checked identical to it on 2e7 random and tie-valued inputs.
 __device__ __forceinline__ float round_f64_to_bf16_value(double t) {
-  unsigned long long u = __double_as_longlong(t);
-  uint32_t hi = (uint32_t)(u >> 32), lo = (uint32_t)u;
-  uint32_t c = ((hi >> 13) & 1u) | (lo != 0u ? 1u : 0u);
-  hi = (hi + 0x0fffu + c) & ~0x1fffu;
-  return (float)__longlong_as_double((long long)((unsigned long long)hi << 32));
+  const uint32_t hi = (uint32_t)((unsigned long long)__double_as_longlong(t) >> 32);
+  const double c = __longlong_as_double((long long)((unsigned long long)((hi & 0xfff00000u) + (45u << 20)) << 32));
+  return (float)((t + c) - c);
 }
 
 // Wave-level exchange through LDS: make this wave's LDS writes visible to its own later reads, without a

@@ -123,6 +123,38 @@ def test_rotate_quant_both_row_layouts(oracle_lib, m, k):
 
 
 @pytest.mark.parametrize("group", [4, 16, 64, 256])
+def test_rotate_quant_rounds_exact_ties_to_even(oracle_lib, group):
+    """Rotated sums that land exactly halfway between two bf16 values, and just beside halfway, at many binades
+    (the once-only rounding of the exact sum, ties to even), in both row layouts."""
+    from hyperflow_h3_flash_amd.int8 import rotate_quant
+
+    rng = np.random.default_rng(group)
+    m, k = 1100, 1024
+    x = np.zeros((m, k), dtype=np.float32)
+    # per group of the row: one large value 2^e * (1 + j/128) and one small value at the half-unit 2^(e-8) (an exact
+    # tie for every output of the group) or at 3 half-units (a tie on the other side), or one quarter-unit off
+    e = rng.integers(-30, 30, size=(m, k // group)).astype(np.float64)
+    big = np.exp2(e) * (1.0 + rng.integers(0, 128, size=e.shape) / 128.0) * rng.choice([-1.0, 1.0], size=e.shape)
+    small = np.exp2(e - 8) * rng.choice([1.0, 3.0, 1.5, 0.5], size=e.shape) * rng.choice([-1.0, 1.0], size=e.shape)
+    x[:, ::group] = big
+    x[:, 1::group] = small
+    bits = oracle_lib.f32_to_bf16(x)
+    assert (oracle_lib.bf16_to_f32(bits) == x).all()  # every input is exactly a bf16 value
+    sx, xq = oracle_lib.quantize(oracle_lib.rotate(bits, group))
+    for rows in (slice(0, 1000), slice(0, m)):  # one workgroup per row (<= 1024 rows), then registers per row
+        q, s = rotate_quant(to_dev_bf16(bits[rows]), group)
+        np.testing.assert_array_equal(s.cpu().numpy(), sx[rows])
+        np.testing.assert_array_equal(q.cpu().numpy(), xq[rows])
+    # the case mix holds: most rotated values were rounded, and a quarter of them sat exactly halfway
+    xr = oracle_lib.bf16_to_f32(oracle_lib.rotate(bits, group)).astype(np.float64)
+    exact = (x.astype(np.float64).reshape(m, k // group, group) @ oracle_lib.regular_hadamard(group)).reshape(m, k)
+    nz = exact != 0
+    assert (xr[nz] != exact[nz]).mean() > 0.5
+    half_units = np.abs(exact[nz]) / np.exp2(np.floor(np.log2(np.abs(exact[nz]))) - 8)
+    assert (half_units % 2 == 1).mean() > 0.2
+
+
+@pytest.mark.parametrize("group", [4, 16, 64, 256])
 def test_rotate_quant_many_rows_every_group(oracle_lib, group):
     """The register-resident layout for each butterfly depth (natural order up to G = 16, transposed for 64, 256)."""
     from hyperflow_h3_flash_amd.int8 import rotate_quant
