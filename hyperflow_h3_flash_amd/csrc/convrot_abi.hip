@@ -547,4 +547,31 @@ int hf_convrot_linear(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t l
   return hf_int8_linear(q_ws, K, w, ldw, sx_ws, sw, u_ws, r, up, ld_up, r, bias, y, ldy, M, N, K, stream);
 }
 
+int64_t hf_convrot_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const int64_t lr = r > 0 ? lowrank_ws_bytes(M, K, std::min<int32_t>(r, hf::kLrRanks)) : 0;
+  return std::max<int64_t>(lr, gemm_ws_bytes(M, N, K));
+}
+
+int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, int32_t quantized, int32_t arithmetic,
+                         const int8_t* w, int64_t ldw, const float* sw, const uint16_t* down, int64_t ld_down,
+                         const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias, int32_t activation,
+                         int32_t group, uint16_t* u, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                         void* ws, int64_t ws_bytes, hf_stream_t stream) {
+  if (M < 0 || N < 0 || K <= 0 || r < 0) return HF_ERR_ARGUMENT;
+  if (M == 0 || N == 0) return HF_OK;
+  int st = HF_OK;
+  if (!quantized) {
+    st = hf_rotate_quant_ex(x, ldx, q, K, sx, M, K, group, arithmetic, stream);
+    if (st != HF_OK) return st;
+  }
+  if (r > 0) {
+    // The low-rank partials and the GEMM's partial planes share the workspace: they are used one after the other.
+    st = lowrank_down_impl(x, ldx, down, ld_down, u, r, M, K, r, ws, ws_bytes, stream);
+    if (st != HF_OK) return st;
+  }
+  return int8_linear_impl(q, K, w, ldw, sx, sw, u, r, up, ld_up, r, bias, y, ldy, M, N, K, ws, ws_bytes, stream,
+                          activation);
+}
+
 }  // extern "C"

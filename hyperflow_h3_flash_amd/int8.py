@@ -177,6 +177,63 @@ class Int8RotLinear(nn.Module):
             cache.update(x=x, version=version, group=self.group, arithmetic=arithmetic, value=quantized)
         return quantized
 
+    def _forward_one_call(self, x: Tensor, x2: Tensor) -> Tensor:
+        """The device layer as one library call (hf_convrot_linear_ws): the same kernels and arithmetic as the
+        rotate_quant / lowrank_down / int8_matmul composition, with the host work of a call done once (the shared
+        quantized input of int8.py:150-159 is handled here the same way)."""
+        _check_group(self.group)
+        M, K = x2.shape
+        N = self.out_features
+        dev = x2.device
+        act = _activation_code(self.activation)
+        _same_device(dev, self.qweight, self.wscale, self.bias)
+        cache = Int8RotLinear._last_input
+        version = None if x.is_inference() else x._version
+        arithmetic = ARITHMETIC_OPTIONS["rotate_quant"]
+        hit = (cache.get("x") is x and cache.get("version") == version and cache.get("group") == self.group
+               and cache.get("arithmetic") == arithmetic)
+        if hit:
+            xq, sx = cache["value"]
+        else:
+            xq = torch.empty(M, K, device=dev, dtype=torch.int8)
+            sx = torch.empty(M, device=dev, dtype=torch.float32)
+        cache.clear()
+        if self.keep_input:
+            cache.update(x=x, version=version, group=self.group, arithmetic=arithmetic, value=(xq, sx))
+        r = self.rank
+        down = up = u = None
+        if r:
+            down, up = self.down.weight, self.up.weight
+            _same_device(dev, down, up)
+            if down.dtype != torch.bfloat16 or not down.is_contiguous():
+                down = down.to(torch.bfloat16).contiguous()
+            if up.dtype != torch.bfloat16 or not up.is_contiguous():
+                up = up.to(torch.bfloat16).contiguous()
+            u = torch.empty(M, r, device=dev, dtype=torch.bfloat16)
+        bias = self.bias
+        if bias is not None and (bias.dtype != torch.bfloat16 or not bias.is_contiguous()):
+            bias = bias.to(torch.bfloat16).contiguous()
+        w, ws_ = self.qweight, self.wscale
+        if not w.is_contiguous():
+            w = w.contiguous()
+        if ws_.dtype != torch.float32 or not ws_.is_contiguous():
+            ws_ = ws_.to(torch.float32).contiguous()
+        y = torch.empty(M, N // 2 if act in _GLU_CODES else N, device=dev, dtype=torch.bfloat16)
+        lib = _native.library()
+        key = (M, N, K, r)
+        nbytes = _ONE_CALL_WS.get(key)
+        if nbytes is None:
+            nbytes = _ONE_CALL_WS[key] = lib.hf_convrot_linear_ws_bytes(M, N, K, r)
+        with torch.cuda.device(dev):
+            work = torch.empty(nbytes, device=dev, dtype=torch.uint8) if nbytes > 0 else None
+            status = lib.hf_convrot_linear_ws(
+                _ptr(x2), x2.stride(0), _ptr(xq), _ptr(sx), int(hit), ROTATE_ARITHMETICS[arithmetic],
+                _ptr(w), w.stride(0), _ptr(ws_), _ptr(down), down.stride(0) if r else 0, _ptr(up),
+                up.stride(0) if r else 0, r, _ptr(bias), act, self.group, _ptr(u), _ptr(y), y.stride(0), M, N, K,
+                _ptr(work), nbytes if work is not None else 0, _stream(dev))
+        _check(status, "hf_convrot_linear_ws")
+        return y
+
     def forward(self, x: Tensor) -> Tensor:
         shape = x.shape
         x2 = x.reshape(-1, self.in_features).to(torch.bfloat16).contiguous()
@@ -187,6 +244,10 @@ class Int8RotLinear(nn.Module):
                 f"(input is on {x2.device})"
             )
         kernels = _kernels()
+        if (kernels.rotate_quant is rotate_quant and kernels.lowrank_down is lowrank_down
+                and kernels.int8_matmul is int8_matmul and self.rank % 8 == 0):
+            y = self._forward_one_call(x, x2)
+            return y.reshape(*shape[:-1], y.shape[-1]).to(x.dtype)
         xq, sx = self._quantize(x, x2, kernels)
         if self.rank:
             u = kernels.lowrank_down(x2, self.down.weight)
@@ -294,6 +355,9 @@ def _pad_rank(u: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
         up = torch.nn.functional.pad(up, (0, pad))
     return u.contiguous(), up.contiguous()
 
+
+#: Workspace bytes of the one-call layer per (M, N, K, rank), asked of the library once.
+_ONE_CALL_WS: dict[tuple[int, int, int, int], int] = {}
 
 #: Output activations the GEMM epilogue applies (the C ABI's HF_ACT_* codes). The gated ones halve the output width.
 ACTIVATIONS = {None: 0, "gelu_tanh": 1, "swiglu": 2, "swiglu_gate_first": 3}

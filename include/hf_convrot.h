@@ -18,6 +18,8 @@
  *   hf_int8_linear_act_ws <- the FFN up-projection + its activation       transformer.py:75-99
  *   hf_int8_gemm_i32  <- the int32 accumulator of `int8_mm_kernel`         int8.py:302-306 (torch._int_mm, :362)
  *   hf_convrot_linear <- `Int8RotLinear.forward` device branch             int8.py:161-171
+ *   hf_convrot_linear_ws <- the same with the shared quantized input,      int8.py:150-171
+ *                        the activation, the arithmetic and a workspace
  */
 #ifndef HF_CONVROT_H
 #define HF_CONVROT_H
@@ -169,6 +171,23 @@ int hf_convrot_linear(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t l
                       const uint16_t* down, int64_t ld_down, const uint16_t* up, int64_t ld_up, int32_t r,
                       const uint16_t* bias, int32_t group, int8_t* q_ws, float* sx_ws, uint16_t* u_ws, uint16_t* y,
                       int64_t ldy, int64_t M, int64_t N, int64_t K, hf_stream_t stream);
+
+/*
+ * The whole layer in one call, with the activation, the rotation arithmetic, the split-K workspace and the shared
+ * quantized input of `Int8RotLinear.forward` (int8.py:150-171):
+ *   quantized == 0: hf_rotate_quant_ex(x -> q [M, K] (ldq = K), sx [M], group, arithmetic);
+ *   quantized != 0: q and sx already hold x's codes and scales (the input shared by q/k/v projections,
+ *                   int8.py:150-159), and x is read only by the low-rank term;
+ * then, when r > 0, hf_lowrank_down_ws(x -> u [M, r] (ldu = r)), then hf_int8_linear_act_ws(q, ..., activation ->
+ * y). `ws` serves both split-K passes (one after the other): hf_convrot_linear_ws_bytes gives its size (a NULL or
+ * smaller workspace runs the unsplit kernels). Same rules as the calls it makes.
+ */
+int64_t hf_convrot_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r);
+int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, int32_t quantized, int32_t arithmetic,
+                         const int8_t* w, int64_t ldw, const float* sw, const uint16_t* down, int64_t ld_down,
+                         const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias, int32_t activation,
+                         int32_t group, uint16_t* u, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                         void* ws, int64_t ws_bytes, hf_stream_t stream);
 
 #ifdef __cplusplus
 }
