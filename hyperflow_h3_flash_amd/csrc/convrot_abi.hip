@@ -250,7 +250,12 @@ struct GemmPlan {
   int splits = 1;
   int k_chunk = 0;
   bool skinny = false;  // at most 64 rows: 128-row weight slices (skinny_gemm_kernel) instead of 256 x 256 tiles
+  double seconds = 0;   // the cost model's estimate of the GEMM's time
 };
+
+constexpr double kPlanBw = 5.0e12;  // sustained HBM bytes per second of the cost model
+// One 128-byte K stage of one 256 x 256 tile at the sustained (power-bound) matrix-core rate.
+constexpr double kTileStageSeconds = 2.0 * 256 * 256 * 128 / (8192.0 * 2.0e9 * 0.55);
 
 GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
   GemmPlan best;
@@ -264,26 +269,25 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
     best.skinny = true;
     best.k_chunk = (int)(chunk * hf::kSkinnyStageK);
     best.splits = (int)((stages + chunk - 1) / chunk);
+    best.seconds = ((double)N * K + 8.0 * best.splits * M * N) / kPlanBw;
     return best;
   }
   const int64_t stages = (K + hf::GBK - 1) / hf::GBK;
   best.k_chunk = (int)(stages * hf::GBK);
   const int64_t tiles = ((M + hf::GBM - 1) / hf::GBM) * ((N + hf::GBN - 1) / hf::GBN);
   const int64_t cus = device_cus();
-  if (tiles >= cus || stages < 4) return best;
-  const double tile_s = 2.0 * hf::GBM * hf::GBN * hf::GBK / (8192.0 * 2.0e9 * 0.55);  // one stage of one tile
-  const double bw = 5.0e12;
   const double fixed_bytes = (double)N * K + (double)M * K + 2.0 * M * N;
-  double best_t = 1e30;
-  for (int64_t s = 1; s <= std::min<int64_t>(stages / 2, hf::kMaxSplits); ++s) {
+  best.seconds = std::max((double)((tiles + cus - 1) / cus) * stages * kTileStageSeconds, fixed_bytes / kPlanBw);
+  if (tiles >= cus || stages < 4) return best;
+  for (int64_t s = 2; s <= std::min<int64_t>(stages / 2, hf::kMaxSplits); ++s) {
     const int64_t chunk = (stages + s - 1) / s;
     const int64_t splits = (stages + chunk - 1) / chunk;
     const double rounds = (double)((tiles * splits + cus - 1) / cus);
-    const double t_mfma = rounds * chunk * tile_s;
-    const double t_mem = (fixed_bytes + (splits > 1 ? 8.0 * splits * M * N : 0.0)) / bw;
+    const double t_mfma = rounds * chunk * kTileStageSeconds;
+    const double t_mem = (fixed_bytes + (splits > 1 ? 8.0 * splits * M * N : 0.0)) / kPlanBw;
     const double t = std::max(t_mfma, t_mem);
-    if (t < best_t * 0.97) {
-      best_t = t;
+    if (t < best.seconds * 0.97) {
+      best.seconds = t;
       best.splits = (int)splits;
       best.k_chunk = (int)(chunk * hf::GBK);
     }
@@ -291,10 +295,37 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
   return best;
 }
 
+// Rows of a many-tile GEMM that run as whole 256 x 256 tiles; the rest (the trailing tile rows) run as a separate
+// few-row GEMM, split over K. The persistent grid takes ceil(tiles / CUs) rounds; when the last round is less than
+// half full, its tiles keep a few CUs busy for a whole tile time while the others idle. Peeling off the trailing
+// tile rows so the main part fills one round fewer, and splitting the peeled rows' K over every CU, turns that round
+// into a fraction of one, plus the partial planes, the finishing pass and a drain between the launches. A lightly
+// loaded last round runs at a higher clock than a full one (the full chip is power-bound), so it is priced at half
+// a round: peeling pays for deep K (M=37710, N=5376, K=14336: 2656 -> 2607 us) and not at K near 5000 (K=5376 and
+// 7168 within 1 %, M=41344, N=13824, K=5120 1 % slower), which this price leaves unpeeled. Returns M when nothing is
+// peeled; the peeled GEMM's workspace is gemm_ws_bytes of the peeled rows.
+int64_t main_gemm_rows(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles_m = (M + hf::GBM - 1) / hf::GBM, tiles_n = (N + hf::GBN - 1) / hf::GBN;
+  const int64_t tiles = tiles_m * tiles_n, cus = device_cus();
+  if (tiles < cus) return M;
+  const int64_t rounds = (tiles + cus - 1) / cus;
+  if (2 * (tiles - (rounds - 1) * cus) > cus) return M;
+  const int64_t rows_main = (rounds - 1) * cus / tiles_n;  // tile rows that fit in one round fewer
+  if (rows_main <= 0 || rows_main >= tiles_m) return M;
+  const int64_t m_tail = M - rows_main * hf::GBM;
+  const GemmPlan tail = gemm_plan(m_tail, N, K);
+  if (tail.splits <= 1) return M;
+  const double t_round = (double)((K + hf::GBK - 1) / hf::GBK) * kTileStageSeconds;
+  const double t_finish = 10e-6 + (8.0 * tail.splits + 2.0) * m_tail * N / kPlanBw;  // launch + partials + output
+  return tail.seconds + t_finish < 0.5 * t_round ? rows_main * hf::GBM : M;
+}
+
 // Ints per split-K partial plane: ceil(M / 32) x ceil(N / 32) blocks of 32 x 32 (partial_block_offset).
 int64_t partial_plane_ints(int64_t M, int64_t N) { return ((M + 31) / 32) * ((N + 31) / 32) * 1024; }
 
 int64_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  const int64_t m_main = main_gemm_rows(M, N, K);
+  if (m_main < M) return gemm_ws_bytes(M - m_main, N, K);
   const GemmPlan p = gemm_plan(M, N, K);
   return (p.splits > 1 || p.skinny) ? (int64_t)p.splits * partial_plane_ints(M, N) * 4 : 0;
 }
@@ -323,6 +354,16 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
   if (glu && (N * ldw >= (int64_t(1) << 32) || (r > 0 && N * ld_up * 2 >= (int64_t(1) << 32)))) return HF_ERR_SIZE;
   const int glu_half = (int)(N / 2), glu_gate_first = act_code == HF_ACT_SWIGLU_GATE_FIRST;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t m_main = main_gemm_rows(M, N, K);
+  if (m_main < M && ws && aligned(ws, 16) && ws_bytes >= gemm_ws_bytes(M - m_main, N, K)) {
+    // The trailing rows as a split-K GEMM (bitwise the same outputs: the partial sums are exact and the finishing
+    // pass applies the same epilogue), then the rest as whole tiles; the same stream orders the two.
+    st = int8_linear_impl(q + m_main * ldq, ldq, w, ldw, sx + m_main, sw, r > 0 ? u + m_main * ldu : u, ldu, up,
+                          ld_up, r, bias, y + m_main * ldy, ldy, M - m_main, N, K, ws, ws_bytes, stream, act_code);
+    if (st != HF_OK) return st;
+    return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, m_main, N, K, nullptr, 0,
+                            stream, act_code);
+  }
   const GemmPlan plan = gemm_plan(M, N, K);
   const int64_t plane = partial_plane_ints(M, N);
   if ((plan.splits > 1 || plan.skinny) && ws && aligned(ws, 16) && ws_bytes >= (int64_t)plan.splits * plane * 4) {

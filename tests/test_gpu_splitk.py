@@ -109,3 +109,50 @@ def test_large_shapes_do_not_split():
     lib = _native.library()
     assert lib.hf_int8_linear_ws_bytes(32768, 15360, 5120) == 0
     assert lib.hf_lowrank_down_ws_bytes(32768, 5120, 64) == 0
+
+
+@pytest.mark.parametrize("m,n,k,r,bias,act", [
+    (37710, 5376, 14336, 0, False, 0),   # the model's FFN down projection at M=37710: 334 trailing rows split over K
+    (37710, 5376, 14336, 64, True, 0),   # with the low-rank term and bias
+    (37408, 5376, 14336, 0, False, 1),   # 32 trailing rows (the skinny kernel), tanh-GELU
+    (37710, 7168, 14336, 32, True, 2),   # SwiGLU: the split partials in pair order
+])
+def test_trailing_tile_rows_split_is_bitwise_the_whole_gemm(oracle_lib, m, n, k, r, bias, act):
+    """Many-tile GEMMs whose last round of the persistent grid would be less than half full run their trailing tile
+    rows as a split-K GEMM (hf_int8_linear_ws_bytes > 0 for them); the result equals the whole unsplit GEMM (no
+    workspace) bitwise, and the oracle on sampled rows of both parts."""
+    from hyperflow_h3_flash_amd import _native
+
+    lib = _native.library()
+    nbytes = lib.hf_int8_linear_ws_bytes(m, n, k)
+    assert nbytes > 0, "the trailing tile rows should take the split path"
+    gen = torch.Generator(device=DEV).manual_seed(m + n + k)
+    q = torch.randint(-127, 128, (m, k), device=DEV, dtype=torch.int8, generator=gen)
+    sx = torch.rand(m, device=DEV, generator=gen) * 1e-2 + 1e-3
+    w = torch.randint(-127, 128, (n, k), device=DEV, dtype=torch.int8, generator=gen)
+    sw = torch.rand(n, device=DEV, generator=gen) * 9e-3 + 1e-3
+    u = (torch.randn(m, r, device=DEV, generator=gen) * 0.5).to(torch.bfloat16) if r else None
+    up = (torch.randn(n, r, device=DEV, generator=gen) * 0.02).to(torch.bfloat16) if r else None
+    b = (torch.randn(n, device=DEV, generator=gen) * 0.01).to(torch.bfloat16) if bias else None
+    n_out = n // 2 if act >= 2 else n
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run(split):
+        y = torch.full((m, n_out), -1, device=DEV, dtype=torch.int16).view(torch.bfloat16)
+        work = torch.empty(nbytes, device=DEV, dtype=torch.uint8) if split else None
+        status = lib.hf_int8_linear_act_ws(p(q), k, p(w), k, p(sx), p(sw), p(u), r, p(up), r, r, p(b), act, p(y),
+                                           n_out, m, n, k, p(work), nbytes if split else 0, stream)
+        assert status == 0
+        torch.cuda.synchronize()
+        return y
+
+    split, whole = run(True), run(False)
+    assert torch.equal(split.view(torch.int16), whole.view(torch.int16))
+    if not r and not bias and not act:
+        tail = m - m % 256
+        rows = np.sort(np.concatenate([np.random.default_rng(m).choice(tail, size=6, replace=False),
+                                       np.random.default_rng(n).choice(np.arange(tail - 512, m), size=6,
+                                                                       replace=False)]))
+        want = oracle_lib.epilogue(oracle_lib.int8_gemm(q[rows].cpu().numpy(), w.cpu().numpy()),
+                                   sx[rows].cpu().numpy(), sw.cpu().numpy())
+        np.testing.assert_array_equal(bits_of(split[rows]), want)
