@@ -65,6 +65,14 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<4>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_lowrank_row_kernel<1>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_lowrank_row_kernel<2>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_lowrank_row_kernel<3>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_lowrank_row_kernel<4>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
 #define HF_LR_ATTR(RB, NW)                                                                                \
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<RB, NW>),             \
                               hipFuncAttributeMaxDynamicSharedMemorySize, hf::lr_lds(NW));
@@ -181,7 +189,13 @@ LrPlan lowrank_plan(int64_t M, int64_t K) {
   return p;
 }
 
+// Few rows: one workgroup per row (lowrank_down_row_kernel), no split and no workspace.
+bool lowrank_by_rows(int64_t M, int64_t K) {
+  return M <= hf::kLrRowMaxRows && K <= (int64_t)hf::kLrRowMaxWaves * 1024;
+}
+
 int64_t lowrank_ws_bytes(int64_t M, int64_t K, int32_t r) {
+  if (lowrank_by_rows(M, K)) return 0;
   const LrPlan p = lowrank_plan(M, K);
   return p.splits > 1 ? (int64_t)p.splits * M * r * 4 : 0;
 }
@@ -195,10 +209,18 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
   if (K % 16 || !aligned(x, 16) || !aligned(down, 16) || (ldx % 8) || (ld_down % 8) || !aligned(u, 8))
     return HF_ERR_ALIGNMENT;
   if (M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (lowrank_by_rows(M, K)) {
+    const int64_t waves = (K + 1023) / 1024, groups = (r + hf::kLrRowRanks - 1) / hf::kLrRowRanks;
+    const int64_t blocks = hf::lowrank_row_blocks(M, r);
+    if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+    hipLaunchKernelGGL(hf::lowrank_down_row_kernel, dim3((unsigned)blocks), dim3((unsigned)(64 * waves)), 0, s, x,
+                       ldx, down, ld_down, u, ldu, (int)M, (int)K, r, (int)groups);
+    return launch_status();
+  }
   if (2 * hf::kLrMaxRows * ldx >= (int64_t(1) << 31) || 2 * hf::kLrRanks * ld_down >= (int64_t(1) << 31))
     return HF_ERR_SIZE;
   allow_large_lds();
-  hipStream_t s = static_cast<hipStream_t>(stream);
   LrPlan plan = lowrank_plan(M, K);
   if (plan.splits > 1 && (!ws || ws_bytes < (int64_t)plan.splits * M * std::min<int32_t>(r, hf::kLrRanks) * 4 ||
                           !aligned(ws, 16))) {
@@ -588,6 +610,52 @@ int hf_convrot_linear(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t l
   return hf_int8_linear(q_ws, K, w, ldw, sx_ws, sw, u_ws, r, up, ld_up, r, bias, y, ldy, M, N, K, stream);
 }
 
+}  // extern "C"
+
+namespace {
+
+// The rotation (bf16_div arithmetic) and the low-rank down projection of a few rows in one launch
+// (rotate_lowrank_row_kernel): the argument rules of hf_rotate_quant and hf_lowrank_down together. Used when both
+// would run their row kernels.
+bool rotate_lowrank_by_rows(int64_t M, int64_t K) {
+  return lowrank_by_rows(M, K) && M <= kRowKernelMaxRows && (K + hf::kRqTile - 1) / hf::kRqTile <= 14;
+}
+
+int rotate_lowrank_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, const uint16_t* down,
+                        int64_t ld_down, uint16_t* u, int64_t ldu, int64_t M, int64_t K, int32_t r, int32_t group,
+                        hf_stream_t stream) {
+  if (M < 0 || K <= 0 || r < 0 || ldx < K || ldq < K || ld_down < K || ldu < r) return HF_ERR_ARGUMENT;
+  if (M == 0) return HF_OK;
+  if (!x || !q || !sx || !down || !u) return HF_ERR_ARGUMENT;
+  const int lg = log4_of(group);
+  if (lg < 0 || K % group) return HF_ERR_GROUP;
+  if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16) || !aligned(down, 16) ||
+      (ld_down % 8) || !aligned(u, 8))
+    return HF_ERR_ALIGNMENT;
+  const int64_t groups = (r + hf::kLrRowRanks - 1) / hf::kLrRowRanks;
+  const int64_t blocks = hf::lowrank_row_blocks(M, r) + M;
+  if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  allow_large_lds();
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const size_t lds = hf::rotate_quant_row_lds_bytes((int)K);
+  const dim3 grid((unsigned)blocks), block((unsigned)(64 * ((K + hf::kRqTile - 1) / hf::kRqTile)));
+#define HF_RLR(G)                                                                                                   \
+  hipLaunchKernelGGL(hf::rotate_lowrank_row_kernel<G>, grid, block, lds, s, x, ldx, q, ldq, sx, down, ld_down, u, \
+                     ldu, (int)M, (int)K, r, (int)groups)
+  switch (lg) {
+    case 1: HF_RLR(1); break;
+    case 2: HF_RLR(2); break;
+    case 3: HF_RLR(3); break;
+    default: HF_RLR(4); break;
+  }
+#undef HF_RLR
+  return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
 int64_t hf_convrot_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const int64_t lr = r > 0 ? lowrank_ws_bytes(M, K, std::min<int32_t>(r, hf::kLrRanks)) : 0;
@@ -602,14 +670,19 @@ int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, i
   if (M < 0 || N < 0 || K <= 0 || r < 0) return HF_ERR_ARGUMENT;
   if (M == 0 || N == 0) return HF_OK;
   int st = HF_OK;
-  if (!quantized) {
-    st = hf_rotate_quant_ex(x, ldx, q, K, sx, M, K, group, arithmetic, stream);
+  if (!quantized && r > 0 && arithmetic == HF_ROTATE_BF16_DIV && rotate_lowrank_by_rows(M, K)) {
+    st = rotate_lowrank_rows(x, ldx, q, K, sx, down, ld_down, u, r, M, K, r, group, stream);
     if (st != HF_OK) return st;
-  }
-  if (r > 0) {
-    // The low-rank partials and the GEMM's partial planes share the workspace: they are used one after the other.
-    st = lowrank_down_impl(x, ldx, down, ld_down, u, r, M, K, r, ws, ws_bytes, stream);
-    if (st != HF_OK) return st;
+  } else {
+    if (!quantized) {
+      st = hf_rotate_quant_ex(x, ldx, q, K, sx, M, K, group, arithmetic, stream);
+      if (st != HF_OK) return st;
+    }
+    if (r > 0) {
+      // The low-rank partials and the GEMM's partial planes share the workspace: they are used one after the other.
+      st = lowrank_down_impl(x, ldx, down, ld_down, u, r, M, K, r, ws, ws_bytes, stream);
+      if (st != HF_OK) return st;
+    }
   }
   return int8_linear_impl(q, K, w, ldw, sx, sw, u, r, up, ld_up, r, bias, y, ldy, M, N, K, ws, ws_bytes, stream,
                           activation);

@@ -9,6 +9,8 @@
 // per CU while one is consumed. Each of the 4 waves multiplies its 32 rows against all ranks with
 // v_mfma_f32_32x32x16_bf16 (first operand down, second x: lanes end with four consecutive rank columns of one row).
 // The MFMA work is a few percent of the stage's memory time; `down` (r x K) streams from L2 once per 128 rows.
+#pragma once
+
 #include "common.h"
 
 namespace hf {
@@ -181,6 +183,106 @@ __global__ __launch_bounds__(256) void lowrank_reduce_kernel(const float* __rest
   for (int s = 0; s < kMaxSplits; ++s)
     if (s < splits) v += p[s];
   u[(int64_t)m * ldu + j] = (uint16_t)f32_to_bf16_rne(v);
+}
+
+// Few rows: a workgroup per row and group of 8 ranks, which needs no second pass. The MFMA kernel above keeps 32 rows
+// per wave, so with few rows it has few row blocks and splits K, and adding the fp32 partials costs another launch.
+// Here wave t of the workgroup takes the 1024-element tile [1024 t, 1024 t + 1024) of x, lane p the 16 consecutive
+// elements from 1024 t + 16 p (K % 16 == 0: all in or all out), loads its 16 elements of the 8 down rows at once (one
+// round trip to memory) and accumulates x[k] down[j, k] in fp32 (fma, k ascending). The 64 lanes' sums are added in a
+// fixed butterfly (lane_fold, then the lane groups of 8, 16 and 32), the waves' sums in wave order through LDS, and
+// each result is rounded to bf16 once (round to nearest even). The order is fixed, so a row's outputs do not depend
+// on the launch it is in (lowrank_down_row_kernel or the rotation's combined row launch). A workgroup reads its row
+// of x (2K bytes) and 8 rows of down (16K bytes), mostly from L2: cheap for a few hundred rows. Measured at M=1024,
+// K=5120, rank 64, the MFMA kernel and its reduction pass are faster (12 us against 19.5 us), hence the row limit.
+// (Two rows per workgroup, sharing the down loads, needed more than the 128 registers a 1024-thread workgroup
+// allows; 16 ranks per workgroup with their loads four ranks ahead took 8.9 us at M=64 against 5.2 us, the
+// rotation included.)
+constexpr int kLrRowMaxRows = 256;  // rows up to which the low-rank down projection runs by rows
+constexpr int kLrRowMaxWaves = 16;  // K <= 16384
+constexpr int kLrRowRanks = 8;      // ranks per workgroup
+
+// One step of the lane butterfly over 2H values: the lanes with bit H set keep the upper H, the others the lower H,
+// and each adds its partner's copy of the kept half.
+template <int H>
+__device__ __forceinline__ void lane_fold(float (&a)[kLrRowRanks], int lane) {
+  const bool upper = lane & H;
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const float keep = upper ? a[H + i] : a[i];
+    const float send = upper ? a[i] : a[H + i];
+    a[i] = keep + __shfl_xor(send, H, 64);
+  }
+}
+
+// u[j] = bf16(sum_k x[k] down[j, k]) of one row (urow) for j in [j0, j0 + 8) and j < r; `sums` is LDS for 8 floats
+// per wave. Every wave of the workgroup calls it.
+__device__ __forceinline__ void lowrank_row_ranks(const uint16_t* __restrict__ xrow,
+                                                  const uint16_t* __restrict__ down, int64_t ld_down,
+                                                  uint16_t* __restrict__ urow, int K, int r, int j0, float* sums) {
+  const int lane = threadIdx.x & 63, t = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // Lanes past K (in the last wave) load in-range elements and contribute zero; ranks past r load row r - 1 and are
+  // not stored. No load is predicated, so all of them issue at once.
+  const bool live = t * 1024 + lane * 16 < K;
+  const int k0 = live ? t * 1024 + lane * 16 : K - 16;
+  const uint4 xa = *reinterpret_cast<const uint4*>(xrow + k0);
+  const uint4 xb = *reinterpret_cast<const uint4*>(xrow + k0 + 8);
+  uint4 d[kLrRowRanks][2];
+#pragma unroll
+  for (int i = 0; i < kLrRowRanks; ++i) {
+    const uint16_t* dr = down + (int64_t)min(j0 + i, r - 1) * ld_down + k0;
+    d[i][0] = *reinterpret_cast<const uint4*>(dr);
+    d[i][1] = *reinterpret_cast<const uint4*>(dr + 8);
+  }
+  const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  float acc[kLrRowRanks];
+#pragma unroll
+  for (int i = 0; i < kLrRowRanks; ++i) {
+    const uint32_t w[8] = {d[i][0].x, d[i][0].y, d[i][0].z, d[i][0].w, d[i][1].x, d[i][1].y, d[i][1].z, d[i][1].w};
+    float v = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v = fmaf(bf16_lo(xw[e]), bf16_lo(w[e]), v);
+      v = fmaf(bf16_hi(xw[e]), bf16_hi(w[e]), v);
+    }
+    acc[i] = live ? v : 0.0f;
+  }
+  lane_fold<4>(acc, lane);
+  lane_fold<2>(acc, lane);
+  lane_fold<1>(acc, lane);
+  // Lane l holds rank j0 + l % 8 over the 8 lanes l ^ (0..7); add the other lane groups of the wave.
+  float total = acc[0] + __shfl_xor(acc[0], 8, 64);
+  total = total + __shfl_xor(total, 16, 64);
+  total = total + __shfl_xor(total, 32, 64);
+  if (lane < kLrRowRanks) sums[t * kLrRowRanks + lane] = total;
+  __syncthreads();
+  if (t == 0 && lane < kLrRowRanks && j0 + lane < r) {
+    float v = sums[lane];
+    for (int w = 1; w < nw; ++w) v += sums[w * kLrRowRanks + lane];
+    urow[j0 + lane] = (uint16_t)f32_to_bf16_rne(v);
+  }
+}
+
+// Workgroups for M rows and r ranks: one per row and group of 8 ranks.
+__host__ __device__ constexpr int64_t lowrank_row_blocks(int64_t M, int r) {
+  return M * ((r + kLrRowRanks - 1) / kLrRowRanks);
+}
+
+// Workgroup b: row b / groups, ranks 8 (b % groups) ... (groups = ceil(r / 8)).
+__device__ __forceinline__ void lowrank_row_block(int64_t b, int groups, const uint16_t* __restrict__ x, int64_t ldx,
+                                                  const uint16_t* __restrict__ down, int64_t ld_down,
+                                                  uint16_t* __restrict__ u, int64_t ldu, int M, int K, int r,
+                                                  float* sums) {
+  const int64_t row = b / groups;
+  lowrank_row_ranks(x + row * ldx, down, ld_down, u + row * ldu, K, r, (int)(b % groups) * kLrRowRanks, sums);
+}
+
+__global__ __launch_bounds__(1024) void lowrank_down_row_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                const uint16_t* __restrict__ down, int64_t ld_down,
+                                                                uint16_t* __restrict__ u, int64_t ldu, int M, int K,
+                                                                int r, int groups) {
+  __shared__ float sums[kLrRowMaxWaves * kLrRowRanks];
+  lowrank_row_block(blockIdx.x, groups, x, ldx, down, ld_down, u, ldu, M, K, r, sums);
 }
 
 // Low-rank up projection y = bf16(u @ up^T + bias), the second half of LowRankLinear.forward

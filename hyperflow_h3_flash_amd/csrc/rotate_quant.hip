@@ -16,7 +16,10 @@
 // registers. For G >= 64 the fp64 pencils go through LDS once so that each lane holds 16 values along digits 2
 // and 3, transformed in registers again. The bf16-rounded values wait in a per-wave row buffer in LDS until the
 // row's absmax is known, then each lane quantizes 16 consecutive values and writes 16 bytes.
+#pragma once
+
 #include "common.h"
+#include "lowrank.hip"
 
 namespace hf {
 
@@ -292,17 +295,15 @@ size_t rotate_quant_row_lds_bytes(int K) {
 }
 
 template <int LOG4G>
-__global__ __launch_bounds__(1024) void rotate_quant_row_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                                int8_t* __restrict__ q, int64_t ldq,
-                                                                float* __restrict__ s, int K) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+__device__ __forceinline__ void rotate_quant_row(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q,
+                                                 int64_t ldq, float* __restrict__ s, int K, int64_t row,
+                                                 unsigned char* smem) {
   const int lane = threadIdx.x & 63;
   const int t = threadIdx.x >> 6;  // this wave's tile
   const int ntiles = blockDim.x >> 6;
   double* scratch = reinterpret_cast<double*>(smem + (size_t)t * kRqScratchBytes);
   uint16_t* rowbuf = reinterpret_cast<uint16_t*>(smem + (size_t)ntiles * kRqScratchBytes);
   float* maxes = reinterpret_cast<float*>(smem + (size_t)ntiles * kRqScratchBytes + 2 * (size_t)ntiles * kRqTile);
-  const int64_t row = blockIdx.x;
   uint4 a, b;
   load_pencil(x + row * ldx, t * kRqTile + lane * 16, K, a, b);
   const float amax = wave_max(rotate_tile<LOG4G>(a, b, t, K, lane, scratch, rowbuf));
@@ -313,6 +314,33 @@ __global__ __launch_bounds__(1024) void rotate_quant_row_kernel(const uint16_t* 
   const RowScale rs = row_scale<LOG4G>(m);
   if (threadIdx.x == 0) s[row] = rs.sx;
   quantize_tile(rowbuf, t, K, lane, rs, q + row * ldq);  // this wave's own tile: its writes are visible to it
+}
+
+template <int LOG4G>
+__global__ __launch_bounds__(1024) void rotate_quant_row_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                int8_t* __restrict__ q, int64_t ldq,
+                                                                float* __restrict__ s, int K) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  rotate_quant_row<LOG4G>(x, ldx, q, ldq, s, K, blockIdx.x, smem);
+}
+
+// The row rotation and the row-wise low-rank down projection (lowrank_row_block) of the same few rows in one launch:
+// both read x and neither depends on the other, so workgroups [0, lowrank_row_blocks) project (row, group of 8
+// ranks) and the next M workgroups rotate a row, side by side on the CUs, in place of two (or, with the split
+// low-rank kernel, three) launches in a row. Each row's results are those of the separate kernels, bit for bit.
+template <int LOG4G>
+__global__ __launch_bounds__(1024) void rotate_lowrank_row_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                  int8_t* __restrict__ q, int64_t ldq,
+                                                                  float* __restrict__ s,
+                                                                  const uint16_t* __restrict__ down, int64_t ld_down,
+                                                                  uint16_t* __restrict__ u, int64_t ldu, int M, int K,
+                                                                  int r, int groups) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int64_t b = blockIdx.x, lr_blocks = lowrank_row_blocks(M, r);
+  if (b < lr_blocks)
+    lowrank_row_block(b, groups, x, ldx, down, ld_down, u, ldu, M, K, r, reinterpret_cast<float*>(smem));
+  else
+    rotate_quant_row<LOG4G>(x, ldx, q, ldq, s, K, b - lr_blocks, smem);
 }
 
 // Many rows, rows up to 20 tiles: the rounded row stays in registers (as fp32) instead of an LDS row buffer, so a
@@ -496,5 +524,14 @@ template __global__ void rotate_quant_row_kernel<1>(const uint16_t*, int64_t, in
 template __global__ void rotate_quant_row_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
 template __global__ void rotate_quant_row_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
 template __global__ void rotate_quant_row_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
+#define HF_RQ_LR_ROW(G)                                                                                             \
+  template __global__ void rotate_lowrank_row_kernel<G>(const uint16_t*, int64_t, int8_t*, int64_t, float*,         \
+                                                        const uint16_t*, int64_t, uint16_t*, int64_t, int, int, int, \
+                                                        int);
+HF_RQ_LR_ROW(1)
+HF_RQ_LR_ROW(2)
+HF_RQ_LR_ROW(3)
+HF_RQ_LR_ROW(4)
+#undef HF_RQ_LR_ROW
 
 }  // namespace hf

@@ -118,3 +118,16 @@ def classify_rotation_mismatches(x_bits: np.ndarray, xr_exact: np.ndarray, xr_ot
         if abs(other - exact) > bound + half_ulp:
             unexplained.append((int(row), int(col), "beyond fp32 accumulation bound"))
     return len(where), unexplained
+
+
+def within_fp32_sum_bound(got: np.ndarray, ref: np.ndarray, x: np.ndarray, d: np.ndarray) -> bool:
+    """Whether bf16 results ``got`` of fp32 sums of K products (rows of x [M, K] against rows of d [R, K], as float
+    values) are within the error of some summation order of the exactly rounded sums ``ref``: recursive fp32 summation
+    in any order is within K 2^-24 sum_k |x_k d_k| of the exact sum, and each result is rounded to bf16 once (2^-7 of
+    |ref| covers both roundings). Near cancellations (an exact sum far below its terms) can only be held to that; a
+    bitwise-fraction check covers the typical element."""
+    x = np.asarray(x, dtype=np.float64)
+    d = np.asarray(d, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    bound = np.abs(ref) * 2.0**-7 + x.shape[1] * 2.0**-24 * (np.abs(x) @ np.abs(d).T)
+    return bool((np.abs(np.asarray(got, dtype=np.float64) - ref) <= bound).all())

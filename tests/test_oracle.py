@@ -493,3 +493,31 @@ def test_swiglu_planted_mistake_is_caught(oracle_lib):
     hidden, gate = t.chunk(2, dim=-1)
     theirs = (hidden * torch.nn.functional.silu(gate)).view(torch.int16).numpy().view(np.uint16)
     assert (oracle_lib.swiglu(y, gate_first=True) != theirs).mean() > 0.5
+
+
+def test_fp32_sum_bound_holds_for_any_order_and_catches_a_dropped_term(oracle_lib):
+    """The device tests' bar for fp32-accumulated low-rank sums (golden_utils.within_fp32_sum_bound): fp32 sums of the
+    same products in a random order and in a pairwise tree, each rounded to bf16, are within it of the oracle's
+    exactly rounded sums; a sum that drops an outlier channel's product is not."""
+    from golden_utils import within_fp32_sum_bound
+
+    m, k, r = 24, 2048, 16
+    inp = oracle_lib.make_inputs(m, k, 8, 256, rank=r, outlier_frac=0.01, outlier_scale=30.0, seed=2)
+    x = oracle_lib.bf16_to_f32(inp["x"]).astype(np.float32)
+    d = oracle_lib.bf16_to_f32(inp["down"]).astype(np.float32)
+    ref = oracle_lib.bf16_to_f32(oracle_lib.lowrank_down(inp["x"], inp["down"]))
+    prods = x[:, None, :] * d[None, :, :]  # exact in fp32: 8-bit significands
+    rng = np.random.default_rng(0)
+    shuffled = np.zeros((m, r), np.float32)
+    for i in rng.permutation(k):
+        shuffled = shuffled + prods[:, :, i]
+    tree = prods.copy()
+    while tree.shape[-1] > 1:
+        tree = tree[..., 0::2] + tree[..., 1::2]
+    for sums in (shuffled, tree[..., 0]):
+        got = oracle_lib.bf16_to_f32(oracle_lib.f32_to_bf16(sums))
+        assert within_fp32_sum_bound(got, ref, x, d)
+    outlier = int(np.argmax(np.abs(x).max(axis=0)))
+    dropped = prods.sum(axis=2, dtype=np.float32) - prods[:, :, outlier]
+    got = oracle_lib.bf16_to_f32(oracle_lib.f32_to_bf16(dropped))
+    assert not within_fp32_sum_bound(got, ref, x, d)
