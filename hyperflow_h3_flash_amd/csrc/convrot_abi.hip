@@ -282,10 +282,11 @@ constexpr double kTileStageSeconds = 2.0 * 256 * 256 * 128 / (8192.0 * 2.0e9 * 0
 GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
   GemmPlan best;
   if (M <= hf::kSkinnyM) {
-    // Enough 128-row x K-chunk work items for two per CU, each chunk at least 4 stages (512 bytes of K).
+    // Enough 128-row x K-chunk work items for one per CU, each chunk at least 4 stages (512 bytes of K). Two per CU
+    // (twice the partial planes to write and add) measured 2.5-4 % slower per layer at M=16..64, N=5120..30720.
     const int64_t stages = (K + hf::kSkinnyStageK - 1) / hf::kSkinnyStageK;
     const int64_t ntiles = (N + hf::kSkinnyN - 1) / hf::kSkinnyN;
-    int64_t want = (2 * device_cus() + ntiles - 1) / ntiles;
+    int64_t want = (device_cus() + ntiles - 1) / ntiles;
     want = std::max<int64_t>(1, std::min<int64_t>(want, std::min<int64_t>(stages / 4, hf::kMaxSplits)));
     const int64_t chunk = (stages + want - 1) / want;
     best.skinny = true;

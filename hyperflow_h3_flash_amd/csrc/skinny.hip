@@ -4,7 +4,7 @@
 //
 // With M <= 64 the weight stream is all the traffic (N x K bytes against 64 x K of activations), so the work is cut
 // into many small weight slices: a work item is 128 weight rows x one K chunk (blockIdx.x = n tile, blockIdx.y =
-// chunk), enough items to give every CU several. A stage is 128 bytes of K for the 128 weight rows and the 64
+// chunk), about as many items as CUs. A stage is 128 bytes of K for the 128 weight rows and the 64
 // activation rows (24 KiB), global -> LDS with buffer_load ... lds as whole 128-byte lines (8 lanes per row), in a
 // 3-stage ring (72 KiB, so two work items share a CU and one's start overlaps the other's tail): two stages in flight
 // while one is multiplied. Wave w multiplies weight rows 32w..32w+31 against all

@@ -38,7 +38,33 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
   const int sub = lane & 31, half = lane >> 5;
   const int m0 = (blockIdx.x / tiles_n) * kSkTileM, n0 = (blockIdx.x % tiles_n) * kSkTileN;
   const int m = m0 + sub;
+  // Every load is issued before the first wait (one round trip to memory, not one per operand): indices are clamped
+  // into the matrices instead of branched on, and values of columns past N or ranks past r are zeroed or not stored.
   const float sxm = sx[min(m, M - 1)];
+  // Bias bits are loaded unconditionally (from wscale's N x 4 bytes when there is no bias: a load in a branch of its
+  // own would be waited for at the branch's end) and converted where they are added.
+  const uint16_t* bsrc = bias ? bias : reinterpret_cast<const uint16_t*>(sw);
+  float wsv[16];
+  uint32_t braw[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int na = col(min(n0 + 8 * (i / 4) + 4 * half + i % 4, N - 1));
+    wsv[i] = sw[na];
+    braw[i] = bsrc[na];
+  }
+  // Low-rank operands of the first 64 ranks, 16 ranks per MFMA: first operand up[n, :], second u[m, :].
+  const bool n_in = n0 + sub < N;
+  const int nrow = col(min(n0 + sub, N - 1)), mrow = min(m, M - 1);
+  v8bf pf[4], uf[4];
+  if (r > 0) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int k = 16 * st + 8 * half;
+      const int kc = min(k, r - 8);
+      pf[st] = *reinterpret_cast<const v8bf*>(up + (int64_t)nrow * ldup + kc);
+      uf[st] = *reinterpret_cast<const v8bf*>(u + (int64_t)mrow * ldu + kc);
+    }
+  }
   // The planes' sums at this lane's 16 positions in block (bm, bn) of each plane (partial_block_offset's layout:
   // each of the wave's loads covers 1 KiB of contiguous memory). Loads are issued eight planes at a time before any
   // is added; the sums are exact in any order.
@@ -52,44 +78,40 @@ __global__ __launch_bounds__(64) void splitk_epilogue_kernel(const int32_t* __re
     for (int s = 0; s < 8; ++s)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq)
-        pl[s][gq] =
-            (s0 + s < splits) ? reinterpret_cast<const v4i*>(blk + (int64_t)(s0 + s) * plane)[64 * gq] : (v4i){0};
+        pl[s][gq] = reinterpret_cast<const v4i*>(blk + (int64_t)min(s0 + s, splits - 1) * plane)[64 * gq];
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sums[4 * gq + e] += pl[s][gq][e];
+        for (int e = 0; e < 4; ++e) sums[4 * gq + e] += (s0 + s < splits) ? pl[s][gq][e] : 0;
   }
   v16f c;
 #pragma unroll
-  for (int gq = 0; gq < 4; ++gq) {
-    const int n = n0 + 8 * gq + 4 * half;
-    const int na = (n < N) ? col(n) : n;
+  for (int i = 0; i < 16; ++i) {
+    const int n = n0 + 8 * (i / 4) + 4 * half + i % 4;
+    c[i] = ((float)sums[i] * sxm) * (n < N ? wsv[i] : 0.0f);
+  }
+  if (r > 0) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float wsn = (n + e < N) ? sw[na + e] : 0.0f;
-      c[4 * gq + e] = ((float)sums[4 * gq + e] * sxm) * wsn;
+    for (int st = 0; st < 4; ++st) {
+      if (16 * st >= r) break;
+      const bool k_in = 16 * st + 8 * half < r;
+      c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k_in && n_in ? pf[st] : (v8bf){0}, k_in && m < M ? uf[st] : (v8bf){0},
+                                                c, 0, 0, 0);
     }
   }
-  // Low-rank term, 16 ranks per MFMA: first operand up[n, :], second u[m, :] (rows past the matrix read zero).
-  const int nrow = (n0 + sub < N) ? col(n0 + sub) : N;
-  for (int kk = 0; kk < r; kk += 16) {
+  for (int kk = 64; kk < r; kk += 16) {  // ranks past 64, loaded as they are used
     const int k = kk + 8 * half;
-    const v8bf pf = (k < r && nrow < N) ? *reinterpret_cast<const v8bf*>(up + (int64_t)nrow * ldup + k) : (v8bf){0};
-    const v8bf uf = (k < r && m < M) ? *reinterpret_cast<const v8bf*>(u + (int64_t)m * ldu + k) : (v8bf){0};
-    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, uf, c, 0, 0, 0);
+    const v8bf p = (k < r && n_in) ? *reinterpret_cast<const v8bf*>(up + (int64_t)nrow * ldup + k) : (v8bf){0};
+    const v8bf q = (k < r && m < M) ? *reinterpret_cast<const v8bf*>(u + (int64_t)m * ldu + k) : (v8bf){0};
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(p, q, c, 0, 0, 0);
   }
   if (m >= M) return;
   if (bias) {
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const int n = n0 + 8 * gq + 4 * half;
-      const int na = (n < N) ? col(n) : n;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (n + e < N) c[4 * gq + e] = c[4 * gq + e] + __uint_as_float((uint32_t)bias[na + e] << 16);
-    }
+    for (int i = 0; i < 16; ++i)
+      if (n0 + 8 * (i / 4) + 4 * half + i % 4 < N) c[i] = c[i] + __uint_as_float(braw[i] << 16);
   }
   if (glu) {
     // Outputs n0 / 2 + 8 gq + 4 h + e from the pair (v, v + 8), v = 4 gq + e.
