@@ -465,8 +465,11 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
   allow_large_lds();
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t ntiles = (K + hf::kRqTile - 1) / hf::kRqTile;
-  if (M <= kRowKernelMaxRows && ntiles <= 14 && M < (int64_t(1) << 31)) {
-    // Few rows: one workgroup per row, one wave per tile.
+  // Few rows: one workgroup per row, one wave per tile, while the rows fit two rounds of workgroups (the row
+  // buffer and transpose areas take up to 157 KiB per workgroup: at M=1024, K=13824 the register kernel below took
+  // 15.8 us against 20.3; at K=5120, two workgroups per CU, the row kernel stays ahead up to 1024 rows).
+  const int64_t row_wgs_per_cu = std::max<int64_t>(1, kMaxLds / (int64_t)hf::rotate_quant_row_lds_bytes((int)K));
+  if (M <= kRowKernelMaxRows && M <= 2 * row_wgs_per_cu * device_cus() && ntiles <= 14) {
     const size_t lds = hf::rotate_quant_row_lds_bytes((int)K);
     const dim3 grid((unsigned)M), block((unsigned)(64 * ntiles));
     switch (lg) {
