@@ -83,9 +83,10 @@ int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_
                     int64_t ldu, int64_t M, int64_t K, int32_t r, hf_stream_t stream);
 
 /*
- * hf_lowrank_down with a caller-provided workspace: with few rows the kernel splits K across workgroups (fp32
- * partial sums in `ws`, added in a fixed order and rounded once to bf16). `hf_lowrank_down_ws_bytes` gives the bytes
- * it uses for these sizes (0: no split); a NULL or smaller workspace runs the unsplit kernel.
+ * hf_lowrank_down with a caller-provided workspace: with a few hundred to a few thousand rows the kernel splits K
+ * across workgroups (fp32 partial sums in `ws`, added in a fixed order and rounded once to bf16); up to 256 rows a
+ * workgroup per row and 8 ranks needs no workspace. `hf_lowrank_down_ws_bytes` gives the bytes it uses for these
+ * sizes (0: no split); a NULL or smaller workspace runs the unsplit kernel.
  * Replaces the same reference interface as hf_lowrank_down (transformer.py:57-58).
  */
 int64_t hf_lowrank_down_ws_bytes(int64_t M, int64_t K, int32_t r);
@@ -121,9 +122,10 @@ int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, c
 /*
  * hf_int8_linear with a caller-provided workspace (16-byte aligned): when the output has fewer 256 x 256 tiles than
  * the device has CUs (few rows), K is split across workgroups; their int32 partial accumulators (`ws`) are added
- * exactly and the same epilogue is applied, so the result equals hf_int8_linear's bit for bit.
- * `hf_int8_linear_ws_bytes` gives the bytes used for these sizes (0: no split); a NULL or smaller workspace runs
- * the unsplit kernel. Replaces the same reference interface as hf_int8_linear (int8.py:376-390).
+ * exactly and the same epilogue is applied, so the result equals hf_int8_linear's bit for bit. With many tiles
+ * whose last round on the CUs would be less than half full and deep K, the trailing tile rows run that way and the
+ * rest as whole tiles. `hf_int8_linear_ws_bytes` gives the bytes used for these sizes (0: no split); a NULL or
+ * smaller workspace runs the unsplit kernel. Replaces the same reference interface as hf_int8_linear (int8.py:376-390).
  */
 int64_t hf_int8_linear_ws_bytes(int64_t M, int64_t N, int64_t K);
 int hf_int8_linear_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
