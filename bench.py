@@ -25,7 +25,7 @@ parity-test shapes and supporting measurements, not the headline line):
   7  the model's own linear shapes (K, N) on the 5.2 s clip's M=37710 tokens, rank 64: q/k/v 5376->7168 each,
      the fused q/k/v 5376->21504, out 7168->5376, gated up 5376->28672, down 14336->5376
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--config N]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--config N [--rows M]]
 """
 
 from __future__ import annotations
@@ -57,6 +57,7 @@ def parse_args():
     p.add_argument("--cpu-rows", type=int, default=32768, help="row sample for the CPU baseline")
     p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6, 7),
                    help="workload: 2 (default) is the headline QKV projection; 1, 3-7 are supporting measurements")
+    p.add_argument("--rows", type=int, default=None, help="--config 5: only this M (64, 256 or 1024)")
     p.add_argument("--copy-probe", action="store_true",
                    help="only copy a 1 GiB device buffer 3 times (calibrates the HBM byte counters) and exit")
     p.add_argument("--vendor-gemm", action="store_true",
@@ -172,7 +173,7 @@ def main():
         copy_probe(torch)
         return
     if args.config != 2:
-        for line in run_config(torch, args.config, args.steps, args.warmup):
+        for line in run_config(torch, args.config, args.steps, args.warmup, rows=args.rows):
             print(json.dumps(line), flush=True)
         return
 
@@ -312,7 +313,7 @@ def linear_bytes(m, k, n, rank, bias):
     return 2 * m * k + n * k + 4 * n + 2 * rank * (k + n) + (2 * n if bias else 0) + 2 * m * n
 
 
-def run_config(torch, config, steps, warmup):
+def run_config(torch, config, steps, warmup, rows=None):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     base = {"n_gpus": 1, "steps": steps, "warmup": warmup, "dtype": "int8", "data": "synthetic (seeded)",
@@ -389,7 +390,7 @@ def run_config(torch, config, steps, warmup):
             torch.cuda.empty_cache()
     else:
         k = 5120
-        for m in (64, 256, 1024):
+        for m in (64, 256, 1024) if rows is None else (rows,):
             for n in (5120, 30720):
                 copies = max(1, -(-(600 << 20) // (n * k)))  # > 600 MB of weights per pass through the copies
                 x, layers = layer_inputs(torch, dev, m, k, n, 32, False, 0.005, 30.0, seed=5, copies=copies)
