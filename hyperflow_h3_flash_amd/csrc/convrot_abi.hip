@@ -81,10 +81,12 @@ void allow_large_lds() {
 #undef HF_LR_ATTR
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_up_kernel),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kUpLds);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel<false>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kSkinnyLds);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel<true>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::kSkinnyLds);
+#define HF_SKINNY_ATTR(GLU, MR)                                                                       \
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel<GLU, MR>),             \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::skinny_lds(MR));
+    HF_SKINNY_ATTR(false, 64) HF_SKINNY_ATTR(true, 64) HF_SKINNY_ATTR(false, 128) HF_SKINNY_ATTR(true, 128)
+    HF_SKINNY_ATTR(false, 256) HF_SKINNY_ATTR(true, 256)
+#undef HF_SKINNY_ATTR
     (void)hipGetLastError();
   });
 }
@@ -271,7 +273,8 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
 struct GemmPlan {
   int splits = 1;
   int k_chunk = 0;
-  bool skinny = false;  // at most 64 rows: 128-row weight slices (skinny_gemm_kernel) instead of 256 x 256 tiles
+  bool skinny = false;  // at most 256 rows: 128-row weight slices (skinny_gemm_kernel) instead of 256 x 256 tiles
+  int mr = 0;           // the skinny kernel's activation rows (64, 128 or 256)
   double seconds = 0;   // the cost model's estimate of the GEMM's time
 };
 
@@ -281,12 +284,17 @@ constexpr double kTileStageSeconds = 2.0 * 256 * 256 * 128 / (8192.0 * 2.0e9 * 0
 
 GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
   GemmPlan best;
-  if (M <= hf::kSkinnyM) {
+  const int64_t ntiles = (N + hf::kSkinnyN - 1) / hf::kSkinnyN;
+  // 128-row weight slices up to 128 rows, and up to 256 rows while the slices leave room to split K at least in two
+  // (one workgroup per CU, one wave per SIMD: with K whole, M=256, N=30720 took 97.7 us against 89.1 us for 256 x 256
+  // tiles split in two; M=256, N=5120 / 15360 took 36.7 / 60.2 us against 40.5 / 65.8 us).
+  if (M <= 128 || (M <= hf::kSkinnyMaxM && 2 * ntiles <= device_cus())) {
     // Enough 128-row x K-chunk work items for one per CU, each chunk at least 4 stages (512 bytes of K). Two per CU
-    // (twice the partial planes to write and add) measured 2.5-4 % slower per layer at M=16..64, N=5120..30720.
+    // (twice the partial planes to write and add) measured 2.5-4 % slower per layer at M=16..64, N=5120..30720. With
+    // more than 64 rows a workgroup fills a CU's LDS, so the items stay within one round (rounded down).
     const int64_t stages = (K + hf::kSkinnyStageK - 1) / hf::kSkinnyStageK;
-    const int64_t ntiles = (N + hf::kSkinnyN - 1) / hf::kSkinnyN;
-    int64_t want = (device_cus() + ntiles - 1) / ntiles;
+    best.mr = M <= hf::kSkinnyM ? hf::kSkinnyM : (M <= 128 ? 128 : hf::kSkinnyMaxM);
+    int64_t want = best.mr == hf::kSkinnyM ? (device_cus() + ntiles - 1) / ntiles : device_cus() / ntiles;
     want = std::max<int64_t>(1, std::min<int64_t>(want, std::min<int64_t>(stages / 4, hf::kMaxSplits)));
     const int64_t chunk = (stages + want - 1) / want;
     best.skinny = true;
@@ -395,13 +403,19 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
     if (plan.skinny) {
       allow_large_lds();
       const dim3 grid((unsigned)((N + hf::kSkinnyN - 1) / hf::kSkinnyN), (unsigned)plan.splits);
-      if (glu)
-        hipLaunchKernelGGL(hf::skinny_gemm_kernel<true>, grid, dim3(256), hf::kSkinnyLds, s, q, ldq, w, ldw,
-                           static_cast<int32_t*>(ws), plane, (int)M, (int)N, (int)K, plan.k_chunk, glu_half,
-                           glu_gate_first);
-      else
-        hipLaunchKernelGGL(hf::skinny_gemm_kernel<false>, grid, dim3(256), hf::kSkinnyLds, s, q, ldq, w, ldw,
-                           static_cast<int32_t*>(ws), plane, (int)M, (int)N, (int)K, plan.k_chunk, 0, 0);
+      int32_t* part = static_cast<int32_t*>(ws);
+      const int gh = glu ? glu_half : 0, gf = glu ? glu_gate_first : 0;
+#define HF_SKINNY_LAUNCH(GLU, MR)                                                                                   \
+  hipLaunchKernelGGL((hf::skinny_gemm_kernel<GLU, MR>), grid, dim3(256), hf::skinny_lds(MR), s, q, ldq, w, ldw,   \
+                     part, plane, (int)M, (int)N, (int)K, plan.k_chunk, gh, gf)
+      if (plan.mr == 64) {
+        if (glu) HF_SKINNY_LAUNCH(true, 64); else HF_SKINNY_LAUNCH(false, 64);
+      } else if (plan.mr == 128) {
+        if (glu) HF_SKINNY_LAUNCH(true, 128); else HF_SKINNY_LAUNCH(false, 128);
+      } else {
+        if (glu) HF_SKINNY_LAUNCH(true, 256); else HF_SKINNY_LAUNCH(false, 256);
+      }
+#undef HF_SKINNY_LAUNCH
       st = launch_status();
     } else {
       hf::GemmArgs a{};

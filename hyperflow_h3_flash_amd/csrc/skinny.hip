@@ -1,33 +1,37 @@
-// INT8 x INT8 -> INT32 partial products for at most 64 rows (timestep / text-conditioning modulation, short audio
+// INT8 x INT8 -> INT32 partial products for at most 256 rows (timestep / text-conditioning modulation, short audio
 // streams): the accumulator of int8_mm_kernel (src/hyperflow_h3_flash/int8.py:302-306) for a K chunk, written as an
 // int32 plane (block by block, partial_block_offset) that splitk_epilogue_kernel adds up and finishes.
 //
-// With M <= 64 the weight stream is all the traffic (N x K bytes against 64 x K of activations), so the work is cut
-// into many small weight slices: a work item is 128 weight rows x one K chunk (blockIdx.x = n tile, blockIdx.y =
-// chunk), about as many items as CUs. A stage is 128 bytes of K for the 128 weight rows and the 64
-// activation rows (24 KiB), global -> LDS with buffer_load ... lds as whole 128-byte lines (8 lanes per row), in a
-// 3-stage ring (72 KiB, so two work items share a CU and one's start overlaps the other's tail): two stages in flight
-// while one is multiplied. Wave w multiplies weight rows 32w..32w+31 against all
-// 64 activation rows: v_mfma_i32_32x32x32_i8 with the weight as the first operand, two blocks per K step.
+// With few rows the weight stream is most of the traffic (N x K bytes against MR x K of activations), so the work is
+// cut into many small weight slices: a work item is 128 weight rows x one K chunk (blockIdx.x = n tile, blockIdx.y =
+// chunk), about as many items as CUs. A stage is 128 bytes of K for the 128 weight rows and the MR activation rows
+// (MR = 64, 128 or 256: 24, 32 or 48 KiB), global -> LDS with buffer_load ... lds as whole 128-byte lines (8 lanes per
+// row), in a 3-stage ring (72, 96 or 144 KiB; with MR = 64 two work items share a CU and one's start overlaps the
+// other's tail): two stages in flight while one is multiplied. Wave w multiplies weight rows 32w..32w+31 against all
+// MR activation rows: v_mfma_i32_32x32x32_i8 with the weight as the first operand, MR / 32 blocks per K step. Against
+// 256 x 256 tiles split over K (the persistent GEMM's few-row mode), 128-row slices give a few-row GEMM four times as
+// many work items before K is split, so fewer partial planes are written and added.
 #include "common.h"
 
 namespace hf {
 
-constexpr int kSkinnyM = 64;                          // activation rows (all of them)
+constexpr int kSkinnyM = 64;                          // activation rows of the smallest form
+constexpr int kSkinnyMaxM = 256;                      // activation rows of the largest form
 constexpr int kSkinnyN = 128;                         // weight rows per work item
 constexpr int kSkinnyStageK = 128;                    // K bytes per stage
 constexpr int kSkinnyWBytes = kSkinnyN * kSkinnyStageK;   // 16 KiB
-constexpr int kSkinnyStageBytes = kSkinnyWBytes + kSkinnyM * kSkinnyStageK;  // 24 KiB
 constexpr int kSkinnyStages = 3;
-constexpr int kSkinnyLds = kSkinnyStages * kSkinnyStageBytes;  // 72 KiB
-constexpr int kSkinnyLoads = 6;                       // per wave and stage: 4 weight blocks + 2 activation blocks
+// LDS per stage and per workgroup for MR activation rows.
+__host__ __device__ constexpr int skinny_stage_bytes(int mr) { return kSkinnyWBytes + mr * kSkinnyStageK; }
+__host__ __device__ constexpr int skinny_lds(int mr) { return kSkinnyStages * skinny_stage_bytes(mr); }
+constexpr int kSkinnyLds = skinny_lds(kSkinnyM);      // 72 KiB
 
 __device__ __forceinline__ int skinny_swz(int r) { return (r & 7) ^ ((r >> 3) & 3); }
 
 // GLU: the weight rows are read in pair order (tile column n is weight row glu_row(n, glu_half, glu_gate_first)),
 // the order the split-K epilogue's SwiGLU pairs columns in.
-template <bool GLU>
-__global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __restrict__ q, int64_t ldq,
+template <bool GLU, int MR = kSkinnyM>
+__global__ __launch_bounds__(256, MR == kSkinnyM ? 2 : 1) void skinny_gemm_kernel(const int8_t* __restrict__ q, int64_t ldq,
                                                              const int8_t* __restrict__ w, int64_t ldw,
                                                              int32_t* __restrict__ acc, int64_t plane, int M, int N,
                                                              int K, int k_chunk, int glu_half, int glu_gate_first) {
@@ -45,15 +49,19 @@ __global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __res
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + (GLU ? 0 : (int64_t)n0 * ldw) + k_lo, bytes_w - (uint32_t)k_lo);
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + k_lo, bytes_q - (uint32_t)k_lo);
 
-  // Stage t -> slot t % 3. Every stage issues 6 loads per wave, stages past the chunk read zeros, so "stage t has
-  // landed" is always vmcnt(6) with the next stage in flight.
+  // Stage t -> slot t % 3. Every stage issues kLoads loads per wave (4 weight blocks and MR / 32 activation blocks
+  // of 1 KiB), stages past the chunk read zeros, so "stage t has landed" is always vmcnt(kLoads) with the next stage
+  // in flight.
+  constexpr int kQBlocks = MR / 32;
+  constexpr int kLoads = 4 + kQBlocks;
+  constexpr int kStageBytes = skinny_stage_bytes(MR);
   auto issue = [&](int t) {
-    unsigned char HF_LDS* st = smem + (t % kSkinnyStages) * kSkinnyStageBytes;
+    unsigned char HF_LDS* st = smem + (t % kSkinnyStages) * kStageBytes;
     const int k0 = t * kSkinnyStageK;
 #pragma unroll
-    for (int i = 0; i < kSkinnyLoads; ++i) {
+    for (int i = 0; i < kLoads; ++i) {
       const bool isq = i >= 4;
-      const int blk = isq ? 2 * wave + (i - 4) : 4 * wave + i;
+      const int blk = isq ? kQBlocks * wave + (i - 4) : 4 * wave + i;
       const int row = 8 * blk + (lane >> 3);
       const int c = (lane & 7) ^ skinny_swz(row);
       const int64_t ld = isq ? ldq : ldw;
@@ -68,23 +76,28 @@ __global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __res
     }
   };
 
-  v16i acc_r[2];
-  acc_r[0] = (v16i){0};
-  acc_r[1] = (v16i){0};
+  v16i acc_r[kQBlocks];
+#pragma unroll
+  for (int jb = 0; jb < kQBlocks; ++jb) acc_r[jb] = (v16i){0};
   const int nst = (k_len + kSkinnyStageK - 1) / kSkinnyStageK;
 #pragma unroll
   for (int t = 0; t < kSkinnyStages - 1; ++t) issue(t);
   const int wrow = wave * 32 + sub;
   for (int t = 0; t < nst; ++t) {
-    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if constexpr (kLoads == 6)
+      asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (kLoads == 8)
+      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     issue(t + kSkinnyStages - 1);
-    const unsigned char HF_LDS* st = smem + (t % kSkinnyStages) * kSkinnyStageBytes;
+    const unsigned char HF_LDS* st = smem + (t % kSkinnyStages) * kStageBytes;
 #pragma unroll
     for (int ks = 0; ks < kSkinnyStageK / 32; ++ks) {
       const int chunk = 2 * ks + half;
       const v4i wf = *(const v4i HF_LDS*)(st + wrow * 128 + ((chunk ^ skinny_swz(wrow)) << 4));
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
+      for (int jb = 0; jb < kQBlocks; ++jb) {
         const int qrow = jb * 32 + sub;
         const v4i qf = *(const v4i HF_LDS*)(st + kSkinnyWBytes + qrow * 128 + ((chunk ^ skinny_swz(qrow)) << 4));
         acc_r[jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, qf, acc_r[jb], 0, 0, 0);
@@ -99,7 +112,7 @@ __global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __res
   const int nbn = (N + 31) / 32, bn = n0 / 32 + wave;
   if (32 * bn >= N) return;
 #pragma unroll
-  for (int jb = 0; jb < 2; ++jb) {
+  for (int jb = 0; jb < kQBlocks; ++jb) {
     if (32 * jb >= M) continue;
     v4i* dst = reinterpret_cast<v4i*>(out + partial_block_offset(jb, bn, nbn) + 4 * lane);
     const v16i& c = acc_r[jb];
@@ -108,9 +121,11 @@ __global__ __launch_bounds__(256, 2) void skinny_gemm_kernel(const int8_t* __res
   }
 }
 
-template __global__ void skinny_gemm_kernel<false>(const int8_t*, int64_t, const int8_t*, int64_t, int32_t*, int64_t,
-                                                   int, int, int, int, int, int);
-template __global__ void skinny_gemm_kernel<true>(const int8_t*, int64_t, const int8_t*, int64_t, int32_t*, int64_t,
-                                                  int, int, int, int, int, int);
+#define HF_SKINNY(GLU, MR)                                                                                          \
+  template __global__ void skinny_gemm_kernel<GLU, MR>(const int8_t*, int64_t, const int8_t*, int64_t, int32_t*,     \
+                                                       int64_t, int, int, int, int, int, int);
+HF_SKINNY(false, 64) HF_SKINNY(true, 64) HF_SKINNY(false, 128) HF_SKINNY(true, 128) HF_SKINNY(false, 256)
+HF_SKINNY(true, 256)
+#undef HF_SKINNY
 
 }  // namespace hf
