@@ -161,8 +161,8 @@ def cpu_baseline(torch, rows, seed=0, m=M, k=K, n=N, rank=RANK, bias=False):
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every run here has one MI355X; "
-              "the linear shards by rows with no communication, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (one MI355X per run; the linear "
+              "shards by rows with no communication, so N GPUs run N independent copies)", file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -1,6 +1,6 @@
 /*
  * ORACLE — test infrastructure only. Nothing in the product imports, links or runs this file: the tests, the
- * smoke check and bench.py's cpu_baseline leg use it as the checker.
+ * smoke check and bench.py's cpu_baseline leg use it for the reference results the device output is compared with.
  *
  * A plain-C restatement of the reference's CPU arithmetic for the INT8 convrot linear,
  * `Int8RotLinear._forward_torch` (src/hyperflow_h3_flash/int8.py:173-179):

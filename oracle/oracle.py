@@ -1,7 +1,8 @@
 """ORACLE — test infrastructure only.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this module, and only as
-the checker. The product (``hyperflow_h3_flash_amd``) never imports it.
+the reference results the device output is compared with (or, in the baseline, as the timed CPU path). The product
+(``hyperflow_h3_flash_amd``) never imports it.
 
 A CPU restatement of the reference's INT8 convrot linear (``Int8RotLinear._forward_torch``,
 src/hyperflow_h3_flash/int8.py:173-179) backed by ``convrot_oracle.c`` (built by ``oracle/Makefile``), plus the
