@@ -86,7 +86,7 @@ def check_gelu(got_bits, pre_bits, lib):
 
 
 # (M, K, N): 256 x 256 tiles with a ragged edge, few rows (split K), at most 64 rows (skinny kernel)
-SHAPES = [(600, 1024, 700), (200, 2048, 512), (40, 1024, 300), (1, 512, 64)]
+SHAPES = [(600, 1024, 700), (200, 2048, 512), (100, 1024, 300), (40, 1024, 300), (1, 512, 64)]
 
 
 @pytest.mark.parametrize("m,k,n", SHAPES)
@@ -160,7 +160,7 @@ def check_swiglu(got_bits, pre_bits, lib, gate_first=False):
 
 
 # (M, K, N), N a multiple of 32: whole tiles, a ragged row and column edge, few rows (split K), the skinny kernel
-GLU_SHAPES = [(600, 1024, 768), (300, 512, 544), (200, 2048, 512), (40, 1024, 320), (1, 512, 64)]
+GLU_SHAPES = [(600, 1024, 768), (300, 512, 544), (200, 2048, 512), (100, 1024, 320), (40, 1024, 320), (1, 512, 64)]
 
 
 @pytest.mark.parametrize("m,k,n", GLU_SHAPES)

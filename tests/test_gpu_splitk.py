@@ -63,7 +63,9 @@ def run_linear(lib, q, w, sx, ws, u, up, bias, split):
 
 @pytest.mark.parametrize("m,n,k,r,bias", [(1, 5120, 5120, 0, False), (64, 5120, 5120, 0, False),
                                           (64, 5000, 5120, 32, True), (200, 3072, 3072, 64, False),
-                                          (37, 1000, 2048, 136, True), (256, 5120, 5120, 32, False)])
+                                          (37, 1000, 2048, 136, True), (256, 5120, 5120, 32, False),
+                                          (100, 3000, 3072, 32, True), (128, 30720, 1024, 0, False),
+                                          (256, 8192, 2048, 0, False)])
 def test_split_gemm_is_bitwise_the_unsplit_gemm(oracle_lib, m, n, k, r, bias):
     from hyperflow_h3_flash_amd import _native
     from hyperflow_h3_flash_amd.int8 import rotate_quant
@@ -105,11 +107,12 @@ def test_split_lowrank_down_matches_oracle(oracle_lib, m, k, r):
 
 
 @pytest.mark.parametrize("m,k,r", [(1, 5120, 32), (7, 1024, 8), (64, 5120, 64), (100, 13824, 32), (256, 5376, 32),
-                                   (33, 16384, 136), (200, 3072, 40), (250, 7168, 64)])
+                                   (33, 16384, 136), (200, 3072, 40), (250, 7168, 64), (9, 2048, 12), (5, 1024, 1)])
 def test_lowrank_down_by_rows_matches_oracle(oracle_lib, m, k, r):
     """Up to 256 rows the down projection runs a workgroup per row and 8 ranks (no split, no workspace): within the
     fp32-sum bound of the oracle's exactly rounded sum, bitwise on almost every element; a partial last 1024-element
-    tile (K=5376), the widest row (K=16384) and rank counts of 1 to 17 groups of 8."""
+    tile (K=5376), the widest row (K=16384), rank counts of 1 to 17 groups of 8 and ranks that are not a multiple
+    of 8 (12, 1)."""
     from hyperflow_h3_flash_amd import _native
     from hyperflow_h3_flash_amd.int8 import lowrank_down
 
