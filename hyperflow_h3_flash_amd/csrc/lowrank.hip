@@ -194,11 +194,12 @@ __global__ __launch_bounds__(256) void lowrank_reduce_kernel(const float* __rest
 // each result is rounded to bf16 once (round to nearest even). The order is fixed, so a row's outputs do not depend
 // on the launch it is in (lowrank_down_row_kernel or the rotation's combined row launch). A workgroup reads its row
 // of x (2K bytes) and 8 rows of down (16K bytes), mostly from L2: cheap for a few hundred rows. Measured at M=1024,
-// K=5120, rank 64, the MFMA kernel and its reduction pass are faster (12 us against 19.5 us), hence the row limit.
+// K=5120, rank 64, the MFMA kernel and its reduction pass are faster (12 us against 19.5 us); whole layers at K=5120,
+// N=5120, rank 32 measured 10 % faster at M=300, 5 % at 384 and equal at 512 by rows, hence the row limit.
 // (Two rows per workgroup, sharing the down loads, needed more than the 128 registers a 1024-thread workgroup
 // allows; 16 ranks per workgroup with their loads four ranks ahead took 8.9 us at M=64 against 5.2 us, the
 // rotation included.)
-constexpr int kLrRowMaxRows = 256;  // rows up to which the low-rank down projection runs by rows
+constexpr int kLrRowMaxRows = 384;  // rows up to which the low-rank down projection runs by rows
 constexpr int kLrRowMaxWaves = 16;  // K <= 16384
 constexpr int kLrRowRanks = 8;      // ranks per workgroup
 

@@ -84,7 +84,7 @@ int hf_lowrank_down(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_
 
 /*
  * hf_lowrank_down with a caller-provided workspace: with a few hundred to a few thousand rows the kernel splits K
- * across workgroups (fp32 partial sums in `ws`, added in a fixed order and rounded once to bf16); up to 256 rows a
+ * across workgroups (fp32 partial sums in `ws`, added in a fixed order and rounded once to bf16); up to 384 rows a
  * workgroup per row and 8 ranks needs no workspace. `hf_lowrank_down_ws_bytes` gives the bytes it uses for these
  * sizes (0: no split); a NULL or smaller workspace runs the unsplit kernel.
  * Replaces the same reference interface as hf_lowrank_down (transformer.py:57-58).

@@ -63,7 +63,7 @@ def make_layer(k, n, group, rank, bias, activation=None, seed=0):
     (300, 1024, 544, 96, False, "swiglu"),  # rank above 64: two low-rank launches
     (257, 512, 300, 0, False, None),
     (100, 5376, 640, 32, True, "gelu_tanh"),  # rotation and low-rank rows in one launch, a partial last tile
-    (256, 5376, 640, 32, False, None),        # the most rows of that launch
+    (256, 5376, 640, 32, False, None),        # 256 rows in that launch
     (3, 14336, 256, 136, False, None),        # its widest row (14 tiles), ranks in nine passes of 16
     (5, 16384, 256, 32, False, None),         # 16 tiles: the rotation's wide-row kernel, the low-rank row kernel
 ])
