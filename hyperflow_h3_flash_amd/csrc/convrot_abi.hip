@@ -406,7 +406,8 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
       int32_t* part = static_cast<int32_t*>(ws);
       const int gh = glu ? glu_half : 0, gf = glu ? glu_gate_first : 0;
 #define HF_SKINNY_LAUNCH(GLU, MR)                                                                                   \
-  hipLaunchKernelGGL((hf::skinny_gemm_kernel<GLU, MR>), grid, dim3(256), hf::skinny_lds(MR), s, q, ldq, w, ldw,   \
+  hipLaunchKernelGGL((hf::skinny_gemm_kernel<GLU, MR>), grid, dim3(64 * hf::skinny_waves(MR)), hf::skinny_lds(MR), \
+                     s, q, ldq, w, ldw,                                                                            \
                      part, plane, (int)M, (int)N, (int)K, plan.k_chunk, gh, gf)
       if (plan.mr == 64) {
         if (glu) HF_SKINNY_LAUNCH(true, 64); else HF_SKINNY_LAUNCH(false, 64);

@@ -7,8 +7,9 @@
 // chunk), about as many items as CUs. A stage is 128 bytes of K for the 128 weight rows and the MR activation rows
 // (MR = 64, 128 or 256: 24, 32 or 48 KiB), global -> LDS with buffer_load ... lds as whole 128-byte lines (8 lanes per
 // row), in a 3-stage ring (72, 96 or 144 KiB; with MR = 64 two work items share a CU and one's start overlaps the
-// other's tail): two stages in flight while one is multiplied. Wave w multiplies weight rows 32w..32w+31 against all
-// MR activation rows: v_mfma_i32_32x32x32_i8 with the weight as the first operand, MR / 32 blocks per K step. Against
+// other's tail): two stages in flight while one is multiplied. Wave w multiplies weight rows 32(w % 4)..+31 against
+// the activation rows (all MR of them with 4 waves; half of them each with the 8 waves of MR = 256):
+// v_mfma_i32_32x32x32_i8 with the weight as the first operand, up to 4 blocks per K step. Against
 // 256 x 256 tiles split over K (the persistent GEMM's few-row mode), 128-row slices give a few-row GEMM four times as
 // many work items before K is split, so fewer partial planes are written and added.
 #include "common.h"
@@ -24,6 +25,9 @@ constexpr int kSkinnyStages = 3;
 // LDS per stage and per workgroup for MR activation rows.
 __host__ __device__ constexpr int skinny_stage_bytes(int mr) { return kSkinnyWBytes + mr * kSkinnyStageK; }
 __host__ __device__ constexpr int skinny_lds(int mr) { return kSkinnyStages * skinny_stage_bytes(mr); }
+// Waves per workgroup: 4 (one per 32 weight rows), 8 with 256 activation rows (the two halves of the rows on
+// different waves, so each SIMD runs two waves while one workgroup fills the CU's LDS).
+__host__ __device__ constexpr int skinny_waves(int mr) { return mr == 256 ? 8 : 4; }
 constexpr int kSkinnyLds = skinny_lds(kSkinnyM);      // 72 KiB
 
 __device__ __forceinline__ int skinny_swz(int r) { return (r & 7) ^ ((r >> 3) & 3); }
@@ -31,7 +35,7 @@ __device__ __forceinline__ int skinny_swz(int r) { return (r & 7) ^ ((r >> 3) & 
 // GLU: the weight rows are read in pair order (tile column n is weight row glu_row(n, glu_half, glu_gate_first)),
 // the order the split-K epilogue's SwiGLU pairs columns in.
 template <bool GLU, int MR = kSkinnyM>
-__global__ __launch_bounds__(256, MR == kSkinnyM ? 2 : 1) void skinny_gemm_kernel(const int8_t* __restrict__ q, int64_t ldq,
+__global__ __launch_bounds__(64 * skinny_waves(MR), MR == kSkinnyM ? 2 : 1) void skinny_gemm_kernel(const int8_t* __restrict__ q, int64_t ldq,
                                                              const int8_t* __restrict__ w, int64_t ldw,
                                                              int32_t* __restrict__ acc, int64_t plane, int M, int N,
                                                              int K, int k_chunk, int glu_half, int glu_gate_first) {
@@ -52,16 +56,20 @@ __global__ __launch_bounds__(256, MR == kSkinnyM ? 2 : 1) void skinny_gemm_kerne
   // Stage t -> slot t % 3. Every stage issues kLoads loads per wave (4 weight blocks and MR / 32 activation blocks
   // of 1 KiB), stages past the chunk read zeros, so "stage t has landed" is always vmcnt(kLoads) with the next stage
   // in flight.
-  constexpr int kQBlocks = MR / 32;
-  constexpr int kLoads = 4 + kQBlocks;
+  constexpr int kWaves = skinny_waves(MR);
+  constexpr int kQBlocks = MR / 32 / (kWaves / 4);     // 32-row activation blocks per wave
+  constexpr int kWLoads = 16 / kWaves;                 // 1 KiB loads per wave and stage: weight
+  constexpr int kQLoads = MR / 8 / kWaves;             // and activations
+  constexpr int kLoads = kWLoads + kQLoads;
   constexpr int kStageBytes = skinny_stage_bytes(MR);
+  const int wn = wave % 4, wm = wave / 4;              // weight rows 32 wn.., activation blocks kQBlocks wm..
   auto issue = [&](int t) {
     unsigned char HF_LDS* st = smem + (t % kSkinnyStages) * kStageBytes;
     const int k0 = t * kSkinnyStageK;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const bool isq = i >= 4;
-      const int blk = isq ? kQBlocks * wave + (i - 4) : 4 * wave + i;
+      const bool isq = i >= kWLoads;
+      const int blk = isq ? kQLoads * wave + (i - kWLoads) : kWLoads * wave + i;
       const int row = 8 * blk + (lane >> 3);
       const int c = (lane & 7) ^ skinny_swz(row);
       const int64_t ld = isq ? ldq : ldw;
@@ -82,14 +90,13 @@ __global__ __launch_bounds__(256, MR == kSkinnyM ? 2 : 1) void skinny_gemm_kerne
   const int nst = (k_len + kSkinnyStageK - 1) / kSkinnyStageK;
 #pragma unroll
   for (int t = 0; t < kSkinnyStages - 1; ++t) issue(t);
-  const int wrow = wave * 32 + sub;
+  const int wrow = wn * 32 + sub;
+  static_assert(kLoads == 6 || kLoads == 8, "wait counts");
   for (int t = 0; t < nst; ++t) {
     if constexpr (kLoads == 6)
       asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr (kLoads == 8)
-      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     else
-      asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     issue(t + kSkinnyStages - 1);
     const unsigned char HF_LDS* st = smem + (t % kSkinnyStages) * kStageBytes;
 #pragma unroll
@@ -98,7 +105,7 @@ __global__ __launch_bounds__(256, MR == kSkinnyM ? 2 : 1) void skinny_gemm_kerne
       const v4i wf = *(const v4i HF_LDS*)(st + wrow * 128 + ((chunk ^ skinny_swz(wrow)) << 4));
 #pragma unroll
       for (int jb = 0; jb < kQBlocks; ++jb) {
-        const int qrow = jb * 32 + sub;
+        const int qrow = (wm * kQBlocks + jb) * 32 + sub;
         const v4i qf = *(const v4i HF_LDS*)(st + kSkinnyWBytes + qrow * 128 + ((chunk ^ skinny_swz(qrow)) << 4));
         acc_r[jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf, qf, acc_r[jb], 0, 0, 0);
       }
@@ -109,12 +116,13 @@ __global__ __launch_bounds__(256, MR == kSkinnyM ? 2 : 1) void skinny_gemm_kerne
   // Lane (sub, h) holds row m = 32jb + sub, columns n0 + 32w + 8g + 4h + (0..3) in registers 4g..4g+3: block
   // (jb, n0 / 32 + w) of this chunk's plane, written whole (partial_block_offset's layout).
   int32_t* out = acc + blockIdx.y * plane;
-  const int nbn = (N + 31) / 32, bn = n0 / 32 + wave;
+  const int nbn = (N + 31) / 32, bn = n0 / 32 + wn;
   if (32 * bn >= N) return;
 #pragma unroll
   for (int jb = 0; jb < kQBlocks; ++jb) {
-    if (32 * jb >= M) continue;
-    v4i* dst = reinterpret_cast<v4i*>(out + partial_block_offset(jb, bn, nbn) + 4 * lane);
+    const int bm = wm * kQBlocks + jb;
+    if (32 * bm >= M) continue;
+    v4i* dst = reinterpret_cast<v4i*>(out + partial_block_offset(bm, bn, nbn) + 4 * lane);
     const v16i& c = acc_r[jb];
 #pragma unroll
     for (int g = 0; g < 4; ++g) dst[64 * g] = (v4i){c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
