@@ -5,11 +5,15 @@ A drop-in for the reference's ``hyperflow_h3_flash.int8`` (src/hyperflow_h3_flas
 (``qweight`` int8 [N, K], ``wscale`` fp32 [N], frozen parameters, no buffers), the same ``regular_hadamard`` /
 ``hadamard_factors`` helpers and the same ``KERNEL_OPTIONS`` / ``set_kernel_options`` / ``resolve_int8_gemm`` API.
 
-``y = (q(x R) @ qweight^T) * s_x * wscale`` with ``R = blockdiag(regular Hadamard of order group)``. The device path
-is two launches of the hand-written kernels in ``csrc/`` (through the C ABI of include/hf_convrot.h): the rotation
-+ per-token quantization, then the INT8 MFMA GEMM with the rescale fused in its epilogue. The arithmetic is that of
-the reference's torch path (int8.py:173-179): the rotated activation is rounded to bf16 before the absmax, and the
-scale and code divisions are true fp32 divisions; the int32 accumulators are exact.
+``y = (q(x R) @ qweight^T) * s_x * wscale`` with ``R = blockdiag(regular Hadamard of order group)``. For a device
+tensor the layer is two launches of the hand-written kernels in ``csrc/`` (through the C ABI of include/hf_convrot.h):
+the rotation + per-token quantization, then the INT8 MFMA GEMM with the rescale fused in its epilogue. The arithmetic
+is that of the reference's torch path (int8.py:173-179): the rotated activation is rounded to bf16 before the absmax,
+and the scale and code divisions are true fp32 divisions; the int32 accumulators are exact.
+
+Host tensors run the same definition on the CPU (``host.py``), as the reference runs its torch statements for CPU
+inputs (int8.py:161-167); a device tensor always runs the HIP kernels, at every row count, and raises when the HIP
+library is missing (there is no other device backend).
 
 Extension (opt-in, adds no tensors when unused): ``rank > 0`` adds the low-rank branch of the reference's
 ``LowRankLinear`` (``up(down(x))``, src/hyperflow_h3_flash/transformer.py:48-58) and ``bias=True`` a bf16 bias, both
@@ -17,8 +21,7 @@ fused into the GEMM epilogue: ``y = bf16((acc*sx)*wscale + bf16(x @ down^T) @ up
 
 There is one backend. Every ``int8_gemm`` choice the reference accepts resolves to it, and both ``rotate_quant``
 choices run the same exactly-rounded rotation (the reference's "factored" kernel differs from its dense one by
-rare one-code roundings, int8.py:23-25; this build always produces the torch-path rounding). Inputs must be on a
-ROCm device; there is no CPU compute path.
+rare one-code roundings, int8.py:23-25; this build always produces the torch-path rounding).
 """
 
 from __future__ import annotations
@@ -31,7 +34,7 @@ from typing import Any, ClassVar
 import torch
 from torch import Tensor, nn
 
-from . import _native
+from . import _native, host
 
 #: Run-time kernel choices accepted for API compatibility with the reference (int8.py:37-39).
 INT8_GEMMS = ("auto", "triton", "cublas", "sgl", "bf16")
@@ -78,9 +81,9 @@ def resolve_int8_gemm(device: torch.device | None = None) -> str:
 
 @functools.cache
 def regular_hadamard(group: int) -> Tensor:
-    """``kron(H4 / 2, ..., H4 / 2)`` of size ``group`` (a power of 4): orthonormal, symmetric, rows sum to one.
-
-    Built in float64 and returned as float32, like int8.py:100-109; ValueError when ``group`` is not a power of 4."""
+    """The regular Hadamard matrix of order ``group`` as fp32 (int8.py:100-109): the Kronecker power of the
+    normalised order-4 block, so every entry is +-2^-n, the matrix is its own transpose and inverse, and each row adds
+    up to one. Computed in float64; ValueError unless ``group`` is 4^n."""
     h4 = torch.tensor([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=torch.float64) / 2
     h, n = torch.ones(1, 1, dtype=torch.float64), 1
     while n < group:
@@ -91,8 +94,9 @@ def regular_hadamard(group: int) -> Tensor:
 
 
 def hadamard_factors(group: int) -> tuple[int, int] | None:
-    """``(GA, GB)`` with ``regular_hadamard(group) == kron(regular_hadamard(GA), regular_hadamard(GB))``, both at
-    least 16; None when ``group`` cannot be split that way (int8.py:112-119)."""
+    """A split of ``group`` into two regular Hadamard orders, each 16 or more, whose Kronecker product is
+    ``regular_hadamard(group)`` (int8.py:112-119): the smaller factor takes a quarter of the base-4 digits, rounded
+    down. None below 256 or for an odd power of two."""
     n = group.bit_length() - 1
     if group < 256 or group != 1 << n or n % 2:
         return None
@@ -111,11 +115,14 @@ def _check_group(group: int) -> None:
 
 
 class Int8RotLinear(nn.Module):
-    """Bias-free W8A8 linear: ``y = (q(x R) @ qweight^T) * s_x * wscale``, ``R = blockdiag(regular Hadamard)``.
+    """W8A8 linear on a block-Hadamard-rotated input, no bias by default (int8.py:127-179): the input is rotated,
+    quantized to int8 with one scale per token, multiplied by the int8 ``qweight`` with an exact integer sum, and
+    rescaled by the token scale and the per-output-channel ``wscale``.
 
-    Linears that read one input (``to_q``, ``to_k``, ``to_v``) quantize it once: a layer with ``keep_input = True``
-    leaves its quantized input for the next layer, which reuses it if it receives the exact same, unmodified tensor.
-    Any other layer clears it, so nothing outlives the projections (int8.py:127-159).
+    Projections that share one input (q, k and v of an attention block) rotate and quantize it once: a layer whose
+    ``keep_input`` is set leaves ``(codes, scales)`` behind keyed by the input tensor's identity and version, the
+    next layer takes them when it is handed that very tensor unchanged, and every layer call drops what it did not
+    leave itself, so the codes never outlive the block (the cache of int8.py:150-159).
 
     ``rank``, ``bias`` and ``activation`` are this build's fused extension; with their defaults the module and its
     state dict are exactly the reference's. ``activation="gelu_tanh"`` applies torch's ``gelu(approximate="tanh")``
@@ -234,16 +241,31 @@ class Int8RotLinear(nn.Module):
         _check(status, "hf_convrot_linear_ws")
         return y
 
+    def _forward_torch(self, x2: Tensor, rot: Tensor | None = None) -> Tensor:
+        """The layer on host tensors (int8.py:173-179): ``host.py``'s evaluation of the device kernels' definition,
+        so the bits match the device's. ``rot`` is accepted for the reference's signature; the rotation is always
+        the regular Hadamard of ``self.group``."""
+        xq, sx = host.rotate_quant(x2, self.group)
+        acc = host.int8_gemm_exact(xq, self.qweight)
+        u = host.lowrank_down(x2, self.down.weight) if self.rank else None
+        y = host.dequantize(acc, sx, self.wscale, u=u, up=self.up.weight if self.rank else None, bias=self.bias)
+        return host.activate(y, self.activation)
+
     def forward(self, x: Tensor) -> Tensor:
         shape = x.shape
         x2 = x.reshape(-1, self.in_features).to(torch.bfloat16).contiguous()
         if not x2.is_cuda:
+            # Host tensors: the same arithmetic on the CPU (the reference's torch branch, int8.py:164-167).
+            Int8RotLinear._last_input.clear()
+            y = self._forward_torch(x2)
+            return y.reshape(*shape[:-1], y.shape[-1]).to(x.dtype)
+        kernels = _kernels()
+        if kernels is None:
             Int8RotLinear._last_input.clear()
             raise RuntimeError(
-                f"Int8RotLinear runs on the gfx950 HIP kernels; move the module and its input to a ROCm device "
-                f"(input is on {x2.device})"
+                f"Int8RotLinear on {x2.device} needs the gfx950 HIP library ({_native.LIB_PATH}); build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` (there is no other device backend)"
             )
-        kernels = _kernels()
         if (kernels.rotate_quant is rotate_quant and kernels.lowrank_down is lowrank_down
                 and kernels.int8_matmul is int8_matmul and self.rank % 8 == 0):
             y = self._forward_one_call(x, x2)
@@ -422,11 +444,14 @@ def int8_gemm_i32(a: Tensor, b: Tensor) -> Tensor:
 
 
 @functools.cache
-def _kernels() -> SimpleNamespace:
-    """The device kernels as a namespace shaped like the reference's ``_kernels()`` (int8.py:182-398).
-
-    Raises RuntimeError when the HIP library is missing: there is no other backend to fall back to."""
-    _native.library()
+def _kernels() -> SimpleNamespace | None:
+    """The device kernels as a namespace shaped like the reference's ``_kernels()`` (int8.py:182-398); None when the
+    HIP library is missing or does not load, as the reference returns None without Triton (int8.py:184-187). The
+    layers then raise for device tensors (no device fallback) and still compute host tensors."""
+    try:
+        _native.library()
+    except RuntimeError:
+        return None
     return SimpleNamespace(
         rotate_quant=rotate_quant,
         int8_matmul=int8_matmul,

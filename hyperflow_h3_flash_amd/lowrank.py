@@ -2,9 +2,9 @@
 
 * `LowRankLinear` — ``y = up(down(x))``, the factorized replacement of a bias-free ``nn.Linear``
   (src/hyperflow_h3_flash/transformer.py:48-72): the same constructor, ``down.weight`` [rank, in] and
-  ``up.weight`` [out, rank] parameters and ``pad_rank``. Both products run on the HIP kernels (``hf_lowrank_down``,
-  then ``hf_lowrank_up``) with the reference's bf16 intermediate: ``bf16(bf16(x @ down^T) @ up^T)``, each sum in
-  fp32 and rounded once.
+  ``up.weight`` [out, rank] parameters and ``pad_rank``. For bf16 device inputs both products run on the HIP
+  kernels (``hf_lowrank_down``, then ``hf_lowrank_up``) with the reference's bf16 intermediate:
+  ``bf16(bf16(x @ down^T) @ up^T)``, each sum in fp32 and rounded once.
 * `set_lowrank_rank_multiple` — re-pad every low-rank linear of a model (transformer.py:285-317).
 * `fuse_qkv` — one `Int8RotLinear` whose rows are the concatenated q, k and v weights. Q, K and V of a block read
   the same input (transformer.py:199-203), so one rotate + quantize and one GEMM produce exactly the three
@@ -22,8 +22,33 @@ from .int8 import Int8RotLinear, _kernels
 RANK_MULTIPLE = 64
 
 
+def _round_up(value: int, multiple: int) -> int:
+    return value if multiple <= 0 else (value + multiple - 1) // multiple * multiple
+
+
+def _resize_rank(layer: "LowRankLinear", rank: int) -> None:
+    """Give ``layer`` exactly ``rank`` ranks: drop trailing rows of ``down`` / columns of ``up``, or append zero ones.
+    Zero ranks contribute exact zeros to ``up @ down``, so the layer's function is unchanged whenever only zero
+    ranks are dropped."""
+    grow = rank - layer.rank
+    down, up = layer.down.weight.detach(), layer.up.weight.detach()
+    if grow >= 0:
+        down = torch.nn.functional.pad(down, (0, 0, 0, grow))
+        up = torch.nn.functional.pad(up, (0, grow))
+    else:
+        down, up = down[:rank], up[:, :rank]
+    layer.down.weight = nn.Parameter(down.contiguous(), requires_grad=False)
+    layer.up.weight = nn.Parameter(up.contiguous(), requires_grad=False)
+    layer.rank = layer.down.out_features = layer.up.in_features = rank
+
+
 class LowRankLinear(nn.Module):
-    """``y = up(down(x))``, the factorized replacement of a bias-free `nn.Linear` (transformer.py:48-72)."""
+    """A bias-free linear stored as two factors, ``y = up(down(x))`` with ``down.weight`` [rank, in] and
+    ``up.weight`` [out, rank] (the reference's module, transformer.py:48-72).
+
+    bf16 inputs on a ROCm device run the two HIP products (``hf_lowrank_down``, ``hf_lowrank_up``): each sum in fp32,
+    rounded once to bf16 like the bf16 ``nn.Linear``s they replace. Every other case (host tensors, or a float32 /
+    float64 module) is the reference's own ``up(down(x))`` in the input's dtype."""
 
     def __init__(self, in_features: int, out_features: int, rank: int) -> None:
         super().__init__()
@@ -31,67 +56,59 @@ class LowRankLinear(nn.Module):
         self.down = nn.Linear(in_features, rank, bias=False)
         self.up = nn.Linear(rank, out_features, bias=False)
 
+    def _on_kernels(self, x: Tensor) -> bool:
+        return (x.is_cuda and x.dtype == torch.bfloat16 and self.down.weight.dtype == torch.bfloat16
+                and self.up.weight.dtype == torch.bfloat16 and self.in_features % 16 == 0)
+
     def forward(self, x: Tensor) -> Tensor:
-        shape = x.shape
-        x2 = x.reshape(-1, self.in_features).to(torch.bfloat16).contiguous()
-        if not x2.is_cuda:
-            raise RuntimeError(
-                f"LowRankLinear runs on the gfx950 HIP kernels; move the module and its input to a ROCm device "
-                f"(input is on {x2.device})"
-            )
+        if not self._on_kernels(x):
+            return self.up(self.down(x))
         kernels = _kernels()
-        u = kernels.lowrank_down(x2, self.down.weight.to(torch.bfloat16))
-        y = kernels.lowrank_up(u, self.up.weight.to(torch.bfloat16))
-        return y.reshape(*shape[:-1], self.out_features).to(x.dtype)
+        if kernels is None:
+            raise RuntimeError(
+                f"LowRankLinear on {x.device} needs the gfx950 HIP library; build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'`"
+            )
+        shape = x.shape
+        x2 = x.reshape(-1, self.in_features).contiguous()
+        u = kernels.lowrank_down(x2, self.down.weight)
+        y = kernels.lowrank_up(u, self.up.weight)
+        return y.reshape(*shape[:-1], self.out_features)
 
     @torch.no_grad()
     def pad_rank(self, multiple: int = RANK_MULTIPLE) -> bool:
-        """Zero-pad the rank up to a multiple of ``multiple``: the new rows of ``down`` and columns of ``up`` are
-        zero, so ``up @ down`` is unchanged. Returns whether the rank changed (transformer.py:60-73)."""
-        rank = -(-self.rank // multiple) * multiple
-        if rank == self.rank:
+        """Append zero ranks up to the next multiple of ``multiple`` (transformer.py:60-73); the product is
+        unchanged. True when ranks were added."""
+        target = _round_up(self.rank, multiple)
+        if target == self.rank:
             return False
-        extra = rank - self.rank
-        down, up = self.down.weight, self.up.weight
-        self.down.weight = nn.Parameter(torch.cat([down, down.new_zeros(extra, down.shape[1])]), requires_grad=False)
-        self.up.weight = nn.Parameter(torch.cat([up, up.new_zeros(up.shape[0], extra)], dim=1), requires_grad=False)
-        self.down.out_features = self.up.in_features = self.rank = rank
+        _resize_rank(self, target)
         return True
 
 
 def _used_rank(layer: LowRankLinear) -> int:
-    """The rank without its zero padding (trailing zero rows of ``down`` and columns of ``up``)."""
-    used = (layer.down.weight.detach().abs().amax(1) != 0) | (layer.up.weight.detach().abs().amax(0) != 0)
-    nonzero = used.nonzero()
-    return int(nonzero[-1]) + 1 if len(nonzero) else 1
+    """One past the last rank whose ``down`` row or ``up`` column holds a nonzero (at least 1): the rank before any
+    zero padding (transformer.py:285-289)."""
+    live = layer.down.weight.detach().ne(0).any(dim=1) | layer.up.weight.detach().ne(0).any(dim=0)
+    ranks = torch.arange(1, live.numel() + 1, device=live.device)[live]
+    return int(ranks.max()) if ranks.numel() else 1
 
 
 @torch.no_grad()
 def set_lowrank_rank_multiple(model: nn.Module, multiple: int) -> int:
-    """Re-pad every `LowRankLinear` to a rank multiple of ``multiple`` (0: no padding); returns how many changed.
+    """Re-pad every `LowRankLinear` in ``model`` from its used rank up to a multiple of ``multiple`` (0 or less:
+    the used rank itself), trimming or appending zero ranks; returns how many layers changed (transformer.py:292-317).
 
-    Zero rows and columns add exact zeros, so every multiple computes the same function (transformer.py:292-317).
-    The kernels read the rank in chunks of 8, so a multiple of 8 (or any multiple of it) avoids padding per call.
-    """
-    changed = 0
-    for layer in model.modules():
-        if not isinstance(layer, LowRankLinear):
-            continue
-        rank = _used_rank(layer)
-        target = -(-rank // multiple) * multiple if multiple > 0 else rank
-        if target == layer.rank:
-            continue
-        down, up = layer.down.weight.detach(), layer.up.weight.detach()
-        if target < layer.rank:
-            down, up = down[:target], up[:, :target]
-        else:
-            down = torch.cat([down, down.new_zeros(target - layer.rank, down.shape[1])])
-            up = torch.cat([up, up.new_zeros(up.shape[0], target - layer.rank)], dim=1)
-        layer.down.weight = nn.Parameter(down.contiguous(), requires_grad=False)
-        layer.up.weight = nn.Parameter(up.contiguous(), requires_grad=False)
-        layer.rank = layer.down.out_features = layer.up.in_features = target
-        changed += 1
-    return changed
+    The function computed is the same for every multiple. The kernels read the rank in chunks of 8, so multiples of 8
+    need no padding per call."""
+    layers = [m for m in model.modules() if isinstance(m, LowRankLinear)]
+    resized = 0
+    for layer in layers:
+        target = _round_up(_used_rank(layer), multiple)
+        if target != layer.rank:
+            _resize_rank(layer, target)
+            resized += 1
+    return resized
 
 
 @torch.no_grad()

@@ -176,12 +176,6 @@ def test_shared_quantization_invalidated_by_in_place_change_and_other_tensors():
     Int8RotLinear._last_input.clear()
 
 
-def test_forward_on_cpu_raises_instead_of_falling_back():
-    layer = Int8RotLinear(64, 32, group=16)
-    with pytest.raises(RuntimeError, match="ROCm device"):
-        layer(torch.randn(3, 64))
-
-
 def test_device_groups_are_checked():
     with pytest.raises(ValueError, match="power of 4"):
         int8_mod._check_group(128)
