@@ -118,3 +118,35 @@ def test_fused_qkv_is_bitwise_the_three_projections(oracle_lib, rank, bias):
         separate = torch.cat([layer(x) for layer in layers], dim=-1)
         together = fused(x)
     assert torch.equal(separate, together)
+
+
+def test_lowrank_linear_keeps_float32_and_float64_precision():
+    """A float32 / float64 LowRankLinear on the device is the reference's ``up(down(x))`` in its own dtype (no
+    rounding to bf16); only bf16 inputs take the HIP kernels."""
+    from hyperflow_h3_flash_amd import LowRankLinear
+
+    torch.manual_seed(5)
+    for dtype in (torch.float32, torch.float64):
+        layer = LowRankLinear(256, 96, 24).to(device=DEV, dtype=dtype)
+        x = torch.randn(7, 3, 256, device=DEV, dtype=dtype)
+        with torch.no_grad():
+            y = layer(x)
+            expected = layer.up(layer.down(x))
+        assert y.dtype == dtype
+        torch.testing.assert_close(y, expected, rtol=0, atol=0)
+
+
+def test_device_layer_without_the_library_raises(monkeypatch):
+    """With no HIP library the layers refuse device tensors (there is no device fallback)."""
+    from hyperflow_h3_flash_amd import Int8RotLinear, LowRankLinear
+    from hyperflow_h3_flash_amd import int8 as int8_mod
+    from hyperflow_h3_flash_amd import lowrank as lowrank_mod
+
+    monkeypatch.setattr(int8_mod, "_kernels", lambda: None)
+    monkeypatch.setattr(lowrank_mod, "_kernels", lambda: None)
+    layer = Int8RotLinear(256, 64, 256).to(DEV)
+    with pytest.raises(RuntimeError, match="HIP library"):
+        layer(torch.randn(4, 256, device=DEV, dtype=torch.bfloat16))
+    lr = LowRankLinear(256, 64, 8).to(device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="HIP library"):
+        lr(torch.randn(4, 256, device=DEV, dtype=torch.bfloat16))

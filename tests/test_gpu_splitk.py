@@ -65,15 +65,19 @@ def run_linear(lib, q, w, sx, ws, u, up, bias, split):
                                           (64, 5000, 5120, 32, True), (200, 3072, 3072, 64, False),
                                           (37, 1000, 2048, 136, True), (256, 5120, 5120, 32, False),
                                           (100, 3000, 3072, 32, True), (128, 30720, 1024, 0, False),
-                                          (256, 8192, 2048, 0, False)])
+                                          (256, 8192, 2048, 0, False),
+                                          # K a multiple of 16 but not of the 128-byte stage: partial last stages
+                                          (64, 4096, 1040, 0, False), (200, 2048, 2064, 0, False),
+                                          (256, 3072, 1040, 32, True), (17, 5000, 2064, 8, False)])
 def test_split_gemm_is_bitwise_the_unsplit_gemm(oracle_lib, m, n, k, r, bias):
     from hyperflow_h3_flash_amd import _native
     from hyperflow_h3_flash_amd.int8 import rotate_quant
 
     lib = _native.library()
-    inp = oracle_lib.make_inputs(m, k, n, 256, rank=r, bias=bias, seed=m + n + r)
+    g = 256 if k % 256 == 0 else 16
+    inp = oracle_lib.make_inputs(m, k, n, g, rank=r, bias=bias, seed=m + n + r)
     x = to_dev_bf16(inp["x"])
-    q, sx = rotate_quant(x, 256)
+    q, sx = rotate_quant(x, g)
     w = torch.from_numpy(inp["qweight"]).to(DEV)
     ws = torch.from_numpy(inp["wscale"]).to(DEV)
     u = up = b = None
@@ -88,8 +92,12 @@ def test_split_gemm_is_bitwise_the_unsplit_gemm(oracle_lib, m, n, k, r, bias):
     whole = run_linear(lib, q, w, sx, ws, u, up, b, False)
     assert torch.equal(split.view(torch.int16), whole.view(torch.int16))
     if not r and not bias:
-        ref = oracle_lib.convrot_linear(inp["x"], inp["qweight"], inp["wscale"], 256)
+        ref = oracle_lib.convrot_linear(inp["x"], inp["qweight"], inp["wscale"], g)
         np.testing.assert_array_equal(bits_of(split), ref["y"])
+    elif not r:
+        ref = oracle_lib.convrot_linear(inp["x"], inp["qweight"], inp["wscale"], g)
+        fused = oracle_lib.fused_epilogue(ref["acc"], ref["sx"], inp["wscale"], None, None, inp["bias"])
+        np.testing.assert_array_equal(bits_of(split), fused)
 
 
 @pytest.mark.parametrize("m,k,r", [(400, 5120, 136), (1100, 5120, 136), (2000, 13824, 32), (1500, 5120, 64)])
