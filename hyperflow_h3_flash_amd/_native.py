@@ -36,6 +36,7 @@ STATUS_NAMES = {
     -3: "HF_ERR_ALIGNMENT",
     -4: "HF_ERR_LAUNCH",
     -5: "HF_ERR_SIZE",
+    -6: "HF_ERR_SCRATCH",
 }
 
 #: Every function include/hf_convrot.h declares, with its ctypes signature.
@@ -62,6 +63,9 @@ SIGNATURES = {
                               _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P], ctypes.c_int),
     "hf_convrot_linear": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _P, _P, _P, _I64, _I64,
                            _I64, _I64, _P], ctypes.c_int),
+    "hf_convrot_linear_noalloc_max_bytes": ([], ctypes.c_int64),
+    "hf_convrot_linear_noalloc": ([_P, _I64, _P, _P, _I32, _I32, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _P, _I32,
+                                   _I32, _P, _P, _I64, _I64, _I64, _I64, _P], ctypes.c_int),
 }
 
 

@@ -461,6 +461,8 @@ const char* hf_strerror(int status) {
     case HF_ERR_ALIGNMENT: return "pointer or stride breaks the 16-byte alignment rules";
     case HF_ERR_LAUNCH: return "HIP kernel launch failed";
     case HF_ERR_SIZE: return "size exceeds the kernels' index range";
+    case HF_ERR_SCRATCH:
+      return "the call needs more workspace than hf_convrot_linear_noalloc's 64 MiB scratch (use hf_convrot_linear_ws)";
     default: return "unknown status";
   }
 }
@@ -705,6 +707,61 @@ int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, i
   }
   return int8_linear_impl(q, K, w, ldw, sx, sw, u, r, up, ld_up, r, bias, y, ldy, M, N, K, ws, ws_bytes, stream,
                           activation);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------- allocation-free entry point
+
+// The workspace of hf_convrot_linear_noalloc: the split-K partial planes and low-rank partial sums of one call, in
+// device memory that the code object itself holds (each device that loads the library keeps its own copy until the
+// process ends). Every call on a device reuses that device's copy; nothing in it needs clearing, since each split
+// writes every element of its partial plane (or partial sums) before the finishing pass reads it.
+constexpr int64_t kScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+
+// The device address of `scratch` on the current device, looked up once per device (the host-side name is a
+// stand-in, not a device address). Null when the lookup fails.
+void* scratch_address() {
+  static std::mutex lock;
+  static void* addr[kMaxScratchDevices] = {nullptr};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return nullptr;
+  std::lock_guard<std::mutex> guard(lock);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t hf_convrot_linear_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int hf_convrot_linear_noalloc(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, int32_t quantized,
+                              int32_t arithmetic, const int8_t* w, int64_t ldw, const float* sw, const uint16_t* down,
+                              int64_t ld_down, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
+                              int32_t activation, int32_t group, uint16_t* u, uint16_t* y, int64_t ldy, int64_t M,
+                              int64_t N, int64_t K, hf_stream_t stream) {
+  if (M < 0 || N < 0 || K <= 0 || r < 0) return HF_ERR_ARGUMENT;
+  if (M == 0 || N == 0) return HF_OK;
+  const int64_t need = hf_convrot_linear_ws_bytes(M, N, K, r);
+  if (need > kScratchBytes) return HF_ERR_SCRATCH;
+  void* ws = need > 0 ? scratch_address() : nullptr;
+  if (need > 0 && !ws) return HF_ERR_LAUNCH;
+  return hf_convrot_linear_ws(x, ldx, q, sx, quantized, arithmetic, w, ldw, sw, down, ld_down, up, ld_up, r, bias,
+                              activation, group, u, y, ldy, M, N, K, ws, need > 0 ? kScratchBytes : 0, stream);
 }
 
 }  // extern "C"

@@ -36,6 +36,7 @@ extern "C" {
 #define HF_ERR_ALIGNMENT (-3) /* a pointer or stride breaks the 16-byte vector-access rules below */
 #define HF_ERR_LAUNCH (-4)    /* the HIP launch failed (hipGetLastError) */
 #define HF_ERR_SIZE (-5)      /* a size exceeds what the kernels index (see each function) */
+#define HF_ERR_SCRATCH (-6)   /* hf_convrot_linear_noalloc: the call needs more than its scratch holds */
 
 typedef void* hf_stream_t; /* hipStream_t */
 
@@ -190,6 +191,22 @@ int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, i
                          const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias, int32_t activation,
                          int32_t group, uint16_t* u, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                          void* ws, int64_t ws_bytes, hf_stream_t stream);
+
+/*
+ * hf_convrot_linear_ws without the workspace argument, for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. It allocates
+ * nothing: the split-K partial planes and low-rank partial sums live in a 64 MiB scratch array inside the library's
+ * code object (hf_convrot_linear_noalloc_max_bytes), one per device, held until the process ends. A call that would
+ * need more than that (hf_convrot_linear_ws_bytes(M, N, K, r) > 64 MiB) returns HF_ERR_SCRATCH and launches nothing.
+ * Calls on one device share its scratch: calls that overlap on one device (other streams, other host threads) race
+ * and must be ordered by the caller. Otherwise exactly hf_convrot_linear_ws with a workspace of the needed size.
+ */
+int64_t hf_convrot_linear_noalloc_max_bytes(void);
+int hf_convrot_linear_noalloc(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, int32_t quantized,
+                              int32_t arithmetic, const int8_t* w, int64_t ldw, const float* sw, const uint16_t* down,
+                              int64_t ld_down, const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias,
+                              int32_t activation, int32_t group, uint16_t* u, uint16_t* y, int64_t ldy, int64_t M,
+                              int64_t N, int64_t K, hf_stream_t stream);
 
 #ifdef __cplusplus
 }
