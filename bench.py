@@ -124,37 +124,104 @@ def read_traffic():
     return None
 
 
-def cpu_baseline(torch, rows, seed=0, m=M, k=K, n=N, rank=RANK, bias=False):
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def onednn_isa() -> str:
+    """The instruction set oneDNN dispatches bf16 matmuls to on this host, from its verbose log of one small bf16
+    matmul run in a child process (ONEDNN_VERBOSE=1); "unknown" when the log has no ISA line."""
+    import subprocess
+
+    code = "import torch; a = torch.randn(64, 64).to(torch.bfloat16); (a @ a).sum()"
+    try:
+        out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120,
+                             env=dict(os.environ, ONEDNN_VERBOSE="1", DNNL_VERBOSE="1")).stdout
+    except (OSError, subprocess.SubprocessError):
+        return "unknown"
+    for line in out.splitlines():
+        if ",info,cpu,isa:" in line:
+            return line.split("isa:", 1)[1].strip()
+    return "unknown"
+
+
+_HOST = {}
+
+
+def host_description(torch) -> str:
+    if not _HOST:
+        _HOST["text"] = (f"torch {torch.__version__} CPU on {cpu_model()}; ATen CPU capability "
+                         f"{torch.backends.cpu.get_cpu_capability()}; oneDNN ISA {onednn_isa()}")
+    return _HOST["text"]
+
+
+def cpu_baseline(torch, rows, seed=0, m=M, k=K, n=N, rank=RANK, bias=False, outlier_frac=0.005,
+                 outlier_scale=30.0, chain=None):
     """The reference's CPU PyTorch path (int8.py:173-179, restated in oracle/torch_path.py) plus the low-rank
-    composition (and a bias), on a `rows`-row sample of an m-row workload: 1 warm-up then the median of 3 timed
-    calls."""
+    composition (and a bias), on a `rows`-row sample of an m-row workload with the same input distributions (x
+    N(0,1) with ceil(outlier_frac * K) outlier channels scaled by outlier_scale): 1 warm-up then the median of 3
+    timed calls. `chain` lists further (K, N, source) layers: source "gelu_tanh" applies torch's tanh-GELU to the
+    previous layer's output and feeds it (an FFN pair), "x" gives the layer its own seeded input of width K (the
+    other linears of a block); the ops of every layer are counted."""
     from oracle import torch_path
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(seed)
-    x = (torch.randn(rows, k, generator=gen)).to(torch.bfloat16)
-    qweight = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=gen)
-    wscale = torch.rand(n, generator=gen) * 9e-3 + 1e-3
-    down = (torch.randn(rank, k, generator=gen) * 0.02).to(torch.bfloat16)
-    up = (torch.randn(n, rank, generator=gen) * 0.02).to(torch.bfloat16)
-    b = (torch.randn(n, generator=gen) * 0.01).to(torch.bfloat16) if bias else None
+
+    def weights(kk, nn):
+        qweight = torch.randint(-127, 128, (nn, kk), dtype=torch.int8, generator=gen)
+        wscale = torch.rand(nn, generator=gen) * 9e-3 + 1e-3
+        down = (torch.randn(rank, kk, generator=gen) * 0.02).to(torch.bfloat16) if rank else None
+        up = (torch.randn(nn, rank, generator=gen) * 0.02).to(torch.bfloat16) if rank else None
+        b = (torch.randn(nn, generator=gen) * 0.01).to(torch.bfloat16) if bias else None
+        return qweight, wscale, down, up, b
+
+    def activations(kk):
+        x = torch.randn(rows, kk, generator=gen)
+        cols = torch.randperm(kk, generator=gen)[: -(-int(round(outlier_frac * 1e4)) * kk // 10000)]
+        x[:, cols] *= outlier_scale
+        return x.to(torch.bfloat16)
+
+    inputs = {}
+    layers = [(k, n, "x", weights(k, n))] + [(kk, nn, src, weights(kk, nn)) for kk, nn, src in (chain or [])]
+    for kk, _, src, _ in layers:
+        if src == "x" and kk not in inputs:
+            inputs[kk] = activations(kk)
+
+    def run():
+        h = None
+        for kk, nn, src, (qw, ws, dn, upw, b) in layers:
+            src_x = torch.nn.functional.gelu(h, approximate="tanh") if src == "gelu_tanh" else inputs[kk]
+            h = torch_path.forward_torch(src_x, qw, ws, GROUP, dn, upw, b)
+        return h
+
     times = []
     for i in range(4):
         t0 = time.perf_counter()
-        torch_path.forward_torch(x, qweight, wscale, GROUP, down, up, b)
+        run()
         t = time.perf_counter() - t0
         if i:
             times.append(t)
     t = statistics.median(times)
+    ops = sum(2.0 * rows * nn * kk for kk, nn, _, _ in layers)
+    shapes = ", ".join(f"K={kk} N={nn}" for kk, nn, _, _ in layers)
     return {
-        "value": round(2.0 * rows * n * k / t / 1e12, 4),
+        "value": round(ops / t / 1e12, 4),
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
-        "sample": f"{rows} of {m} rows (K={k}, N={n}, G={GROUP}, rank {rank}{', bias' if bias else ''}); median of "
-                  f"3 after 1 warm-up, {t:.3f} s per call; torch {torch.__version__} CPU, "
-                  f"{platform.processor() or platform.machine()}",
+        "sample": f"{rows} of {m} rows ({shapes}, G={GROUP}, rank {rank}{', bias' if bias else ''}, "
+                  f"{outlier_frac * 100:g}% outlier channels x{outlier_scale:g}); median of 3 after 1 warm-up, "
+                  f"{t:.3f} s per call; {host_description(torch)}",
     }
 
 
@@ -173,7 +240,8 @@ def main():
         copy_probe(torch)
         return
     if args.config != 2:
-        for line in run_config(torch, args.config, args.steps, args.warmup, rows=args.rows):
+        for line in run_config(torch, args.config, args.steps, args.warmup, rows=args.rows,
+                               cpu_rows=0 if args.no_cpu_baseline else args.cpu_rows):
             print(json.dumps(line), flush=True)
         return
 
@@ -255,7 +323,7 @@ def main():
             "bound": "mfma",
             "achieved": round(gemm_tops, 2),
             "peak": PEAK_INT8_TOPS,
-            "unit": "TFLOP/s",
+            "unit": "TOPS",
             "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
             "traffic": read_traffic(),
         },
@@ -313,7 +381,7 @@ def linear_bytes(m, k, n, rank, bias):
     return 2 * m * k + n * k + 4 * n + 2 * rank * (k + n) + (2 * n if bias else 0) + 2 * m * n
 
 
-def run_config(torch, config, steps, warmup, rows=None):
+def run_config(torch, config, steps, warmup, rows=None, cpu_rows=2048):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     base = {"n_gpus": 1, "steps": steps, "warmup": warmup, "dtype": "int8", "data": "synthetic (seeded)",
@@ -324,7 +392,7 @@ def run_config(torch, config, steps, warmup, rows=None):
         with torch.no_grad():
             t = timed(torch, lambda: layer(x), steps, warmup)
         # the reference's own CPU-runnable case: its CPU path over all 1024 rows, beside the device figure
-        cpu = cpu_baseline(torch, m, seed=1, m=m, k=k, n=n, rank=r, bias=True)
+        cpu = cpu_baseline(torch, m, seed=1, m=m, k=k, n=n, rank=r, bias=True, outlier_frac=0.01, outlier_scale=20.0)
         yield dict(base, metric="convrot INT8 linear TOPS, M=1024 K=3072 N=3072", unit="TOPS",
                    value=round(2.0 * m * n * k / t / 1e12, 2), ms_per_step=round(t * 1e3, 4), higher_is_better=True,
                    hbm_GBs=round(linear_bytes(m, k, n, r, True) / t / 1e9, 1), cpu_baseline=cpu,
@@ -368,8 +436,19 @@ def run_config(torch, config, steps, warmup, rows=None):
             extra = {"unfused_ms_per_step": round(t_unfused * 1e3, 4)}
         t = timed(torch, step, steps, warmup)
         ops = sum(2.0 * m * n * k for k, n in shapes)
+        cpu = None
+        if cpu_rows and config in (3, 4):
+            del xs, layers, built
+            torch.cuda.empty_cache()
+            k0, n0 = shapes[0]
+            if config == 3:
+                chain = [(shapes[1][0], shapes[1][1], "gelu_tanh")]
+            else:
+                chain = [(shapes[1][0], shapes[1][1], "x"), (shapes[2][0], shapes[2][1], "x"),
+                         (shapes[3][0], shapes[3][1], "x")]
+            cpu = cpu_baseline(torch, min(cpu_rows, 2048), seed=3, m=m, k=k0, n=n0, rank=64, chain=chain)
         yield dict(base, metric=f"convrot INT8 {name} TOPS, M={m}", unit="TOPS", value=round(ops / t / 1e12, 2),
-                   ms_per_step=round(t * 1e3, 4), higher_is_better=True,
+                   ms_per_step=round(t * 1e3, 4), higher_is_better=True, cpu_baseline=cpu,
                    pct_of_peak=round(100.0 * ops / t / 1e12 / PEAK_INT8_TOPS, 2), **extra,
                    config={"workload": name, "M": m, "shapes_KN": shapes, "group": GROUP, "rank": 64,
                            "bias": False,
@@ -406,10 +485,12 @@ def run_config(torch, config, steps, warmup, rows=None):
                             layer(x)
                 t = timed(torch, graph.replay, steps, warmup) / copies
                 nbytes = linear_bytes(m, k, n, 32, False)
+                del graph
+                cpu = cpu_baseline(torch, m, seed=5, m=m, k=k, n=n, rank=32) if cpu_rows else None
                 yield dict(base, metric=f"convrot INT8 linear HBM GB/s, M={m} K={k} N={n}", unit="GB/s",
                            value=round(nbytes / t / 1e9, 1), ms_per_step=round(t * 1e3, 4), higher_is_better=True,
                            pct_of_hbm_peak=round(100.0 * nbytes / t / 1e9 / PEAK_HBM_GBS, 2),
-                           tops=round(2.0 * m * n * k / t / 1e12, 2),
+                           tops=round(2.0 * m * n * k / t / 1e12, 2), cpu_baseline=cpu,
                            config={"workload": "small-M convrot linear", "M": m, "K": k, "N": n, "group": GROUP,
                                    "rank": 32, "bias": False, "weight_copies": copies})
                 del x, layers
