@@ -5,6 +5,7 @@
 #include "../../include/hf_convrot.h"
 #include "int8_gemm.hip"
 #include "lowrank.hip"
+#include "mid_gemm.hip"
 #include "rotate_quant.hip"
 #include "skinny.hip"
 #include "splitk.hip"
@@ -81,6 +82,10 @@ void allow_large_lds() {
 #undef HF_LR_ATTR
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_up_kernel),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kUpLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::mid_gemm_kernel<hf::kActNone>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::kMidLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::mid_gemm_kernel<hf::kActGeluTanh>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::kMidLds);
 #define HF_SKINNY_ATTR(GLU, MR)                                                                       \
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel<GLU, MR>),             \
                               hipFuncAttributeMaxDynamicSharedMemorySize, hf::skinny_lds(MR));
@@ -326,6 +331,20 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
   return best;
 }
 
+// Whether a GEMM runs as 256 x 128 tiles (mid_gemm_kernel): its 256 x 256 tiles are fewer than the CUs, it is too
+// tall for the 128-row weight slices (skinny_gemm_kernel), and the 256 x 128 tiles fill at least half the CUs, so no
+// K split (with its int32 partial planes and finishing pass) is needed. The kernel's epilogue covers rank <= 64 and
+// the tanh-GELU; gated (SwiGLU) outputs keep the split path.
+bool use_mid_gemm(int64_t M, int64_t N, int32_t r, bool glu) {
+  if (glu || r > 64) return false;
+  const int64_t cus = device_cus();
+  const int64_t tiles_m = (M + hf::GBM - 1) / hf::GBM;
+  if (tiles_m * ((N + hf::GBN - 1) / hf::GBN) >= cus) return false;
+  const int64_t ntiles = (N + hf::kSkinnyN - 1) / hf::kSkinnyN;
+  if (M <= 128 || (M <= hf::kSkinnyMaxM && 2 * ntiles <= cus)) return false;
+  return 2 * tiles_m * ((N + hf::kMidBN - 1) / hf::kMidBN) >= cus;
+}
+
 // Rows of a many-tile GEMM that run as whole 256 x 256 tiles; the rest (the trailing tile rows) run as a separate
 // few-row GEMM, split over K. The persistent grid takes ceil(tiles / CUs) rounds; when the last round is less than
 // half full, its tiles keep a few CUs busy for a whole tile time while the others idle. Peeling off the trailing
@@ -394,6 +413,22 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
     if (st != HF_OK) return st;
     return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, m_main, N, K, nullptr, 0,
                             stream, act_code);
+  }
+  if (use_mid_gemm(M, N, r, glu)) {
+    allow_large_lds();
+    hf::MidArgs a{};
+    a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.sx = sx; a.sw = sw;
+    a.u = r > 0 ? u : nullptr; a.ldu = ldu; a.up = r > 0 ? up : nullptr; a.ldup = ld_up; a.r = r;
+    a.bias = bias; a.y = y; a.ldy = ldy; a.M = (int)M; a.N = (int)N; a.K = (int)K;
+    a.tiles_m = (int)((M + hf::kMidBM - 1) / hf::kMidBM);
+    a.tiles_n = (int)((N + hf::kMidBN - 1) / hf::kMidBN);
+    a.out_vec16 = aligned(y, 16) && (ldy % 8) == 0;
+    const dim3 grid((unsigned)((int64_t)a.tiles_m * a.tiles_n)), block(hf::kMidThreads);
+    if (act == hf::kActGeluTanh)
+      hipLaunchKernelGGL(hf::mid_gemm_kernel<hf::kActGeluTanh>, grid, block, hf::kMidLds, s, a);
+    else
+      hipLaunchKernelGGL(hf::mid_gemm_kernel<hf::kActNone>, grid, block, hf::kMidLds, s, a);
+    return launch_status();
   }
   const GemmPlan plan = gemm_plan(M, N, K);
   const int64_t plane = partial_plane_ints(M, N);
