@@ -26,6 +26,9 @@ int log4_of(int32_t group) {
     case 16: return 2;
     case 64: return 3;
     case 256: return 4;
+    case 1024: return 5;
+    case 4096: return 6;
+    case 16384: return 7;
     default: return -1;
   }
 }
@@ -82,6 +85,10 @@ void allow_large_lds() {
 #undef HF_LR_ATTR
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_up_kernel),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kUpLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_wide_kernel<false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_wide_kernel<true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::mid_gemm_kernel<hf::kActNone>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, hf::kMidLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::mid_gemm_kernel<hf::kActGeluTanh>),
@@ -94,6 +101,21 @@ void allow_large_lds() {
 #undef HF_SKINNY_ATTR
     (void)hipGetLastError();
   });
+}
+
+// Groups of 1024 and more: rotate_quant_wide_kernel, one workgroup per row with the row's fp64 sums in LDS
+// (K * 8 bytes, so K <= 20472). The caller has checked the group, the alignment and M > 0.
+int launch_rotate_wide(bool f32_recip, int lg, const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx,
+                       int64_t M, int64_t K, hipStream_t s) {
+  const size_t lds = hf::rotate_quant_wide_lds_bytes((int)std::min<int64_t>(K, 1 << 20));
+  if (lds > (size_t)kMaxLds || M >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  allow_large_lds();
+  const dim3 grid((unsigned)M), block(hf::kRqWideThreads);
+  if (f32_recip)
+    hipLaunchKernelGGL(hf::rotate_quant_wide_kernel<true>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K, lg);
+  else
+    hipLaunchKernelGGL(hf::rotate_quant_wide_kernel<false>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K, lg);
+  return launch_status();
 }
 
 // rotate_quant_reg_kernel<lg, tpw> (both already range-checked by the caller).
@@ -492,7 +514,7 @@ const char* hf_strerror(int status) {
   switch (status) {
     case HF_OK: return "ok";
     case HF_ERR_ARGUMENT: return "invalid argument (null pointer, negative size or stride smaller than the row)";
-    case HF_ERR_GROUP: return "unsupported Hadamard group (4, 16, 64 or 256, dividing K)";
+    case HF_ERR_GROUP: return "unsupported Hadamard group (a power of 4 from 4 to 16384, dividing K)";
     case HF_ERR_ALIGNMENT: return "pointer or stride breaks the 16-byte alignment rules";
     case HF_ERR_LAUNCH: return "HIP kernel launch failed";
     case HF_ERR_SIZE: return "size exceeds the kernels' index range";
@@ -510,6 +532,7 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
   const int lg = log4_of(group);
   if (lg < 0 || K % group) return HF_ERR_GROUP;
   if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16)) return HF_ERR_ALIGNMENT;
+  if (lg >= 5) return launch_rotate_wide(false, lg, x, ldx, q, ldq, sx, M, K, static_cast<hipStream_t>(stream));
   int waves = 4;
   while (waves > 0 && hf::rotate_quant_lds_bytes(waves, (int)std::min<int64_t>(K, 1 << 30)) > (size_t)kMaxLds)
     waves >>= 1;
@@ -567,6 +590,7 @@ int hf_rotate_quant_ex(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, f
   if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16)) return HF_ERR_ALIGNMENT;
   if (K >= (int64_t(1) << 30)) return HF_ERR_SIZE;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (lg >= 5) return launch_rotate_wide(true, lg, x, ldx, q, ldq, sx, M, K, s);
   constexpr int waves = 4;
   const size_t lds = hf::rotate_quant_f32_recip_lds_bytes(waves);
   const unsigned blocks = (unsigned)std::min<int64_t>((M + waves - 1) / waves, int64_t(1) << 30);
@@ -684,7 +708,7 @@ int rotate_lowrank_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, 
   if (M == 0) return HF_OK;
   if (!x || !q || !sx || !down || !u) return HF_ERR_ARGUMENT;
   const int lg = log4_of(group);
-  if (lg < 0 || K % group) return HF_ERR_GROUP;
+  if (lg < 0 || lg > 4 || K % group) return HF_ERR_GROUP;
   if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16) || !aligned(down, 16) ||
       (ld_down % 8) || !aligned(u, 8))
     return HF_ERR_ALIGNMENT;
@@ -726,7 +750,7 @@ int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, i
   if (M < 0 || N < 0 || K <= 0 || r < 0) return HF_ERR_ARGUMENT;
   if (M == 0 || N == 0) return HF_OK;
   int st = HF_OK;
-  if (!quantized && r > 0 && arithmetic == HF_ROTATE_BF16_DIV && rotate_lowrank_by_rows(M, K)) {
+  if (!quantized && r > 0 && arithmetic == HF_ROTATE_BF16_DIV && group <= 256 && rotate_lowrank_by_rows(M, K)) {
     st = rotate_lowrank_rows(x, ldx, q, K, sx, down, ld_down, u, r, M, K, r, group, stream);
     if (st != HF_OK) return st;
   } else {

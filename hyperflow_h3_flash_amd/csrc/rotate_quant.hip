@@ -183,13 +183,17 @@ struct RowScale {
   float sx, d, inv;
 };
 
-template <int LOG4G>
-__device__ __forceinline__ RowScale row_scale(float amax) {
+__device__ __forceinline__ RowScale row_scale_n(float amax, int log4g) {
   RowScale r;
-  r.sx = fmaxf(ldexpf(amax, -LOG4G), 1e-12f) / 127.0f;
-  r.d = ldexpf(r.sx, LOG4G);  // (t * 2^n) / (sx * 2^n) == xr / sx exactly
+  r.sx = fmaxf(ldexpf(amax, -log4g), 1e-12f) / 127.0f;
+  r.d = ldexpf(r.sx, log4g);  // (t * 2^n) / (sx * 2^n) == xr / sx exactly
   r.inv = 1.0f / r.d;         // correctly rounded; the per-element quotients use it
   return r;
+}
+
+template <int LOG4G>
+__device__ __forceinline__ RowScale row_scale(float amax) {
+  return row_scale_n(amax, LOG4G);
 }
 
 // Quantizes 8 packed bf16 pairs (int8.py:178): value v = 2i + h of the pairs becomes byte v % 4 of out[v / 4].
@@ -431,10 +435,15 @@ void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t
     amax = fmaxf(amax, rotate_tile_rounded<LOG4G>(a, b, lane, scratch, held[i]));
   }
   amax = wave_max(amax);
-  if (lane == 0) maxes[wave] = amax;
-  __syncthreads();
-  float m = 0.0f;
-  for (int w = 0; w < wpr; ++w) m = fmaxf(m, maxes[(wave / wpr) * wpr + w]);
+  float m = amax;
+  if (wpr > 1) {
+    // The waves of a row combine their maxima. With one wave per row there is nothing to combine and no barrier:
+    // the workgroup's waves (rows) run independently.
+    if (lane == 0) maxes[wave] = amax;
+    __syncthreads();
+    m = 0.0f;
+    for (int w = 0; w < wpr; ++w) m = fmaxf(m, maxes[(wave / wpr) * wpr + w]);
+  }
   if (!live) return;
   const RowScale rs = row_scale<LOG4G>(m);
   if (part == 0 && lane == 0) s[row] = rs.sx;
@@ -496,6 +505,88 @@ __global__ __launch_bounds__(256) void rotate_quant_f32_recip_kernel(const uint1
 
 size_t rotate_quant_f32_recip_lds_bytes(int waves) { return (size_t)waves * kRqScratchBytes; }
 
+// Hadamard groups of 4^5 = 1024 elements and more (a group spans one or more whole 1024-element tiles): one
+// workgroup per row keeps the row's unnormalised fp64 sums in LDS, 8 bytes per element. Each thread loads 16
+// consecutive elements and transforms digits 0-1 in registers; every higher digit of the in-group index is then a
+// radix-4 pass over the LDS row (stride 4^d; consecutive threads take consecutive quadruples), a barrier between
+// passes. The butterflies are those of the tile kernels (exact while a group's nonzero inputs span at most
+// 53 - 8 - 2 log4(G) binades). The rounding and quantization are rotate_quant_kernel's (each sum rounded once to bf16,
+// true division) or, with F32_RECIP, rotate_quant_f32_recip_kernel's (rounded once to fp32, reciprocal multiply).
+constexpr int kRqWideThreads = 256;
+size_t rotate_quant_wide_lds_bytes(int K) { return 8 * (size_t)K + 4 * sizeof(float); }
+
+template <bool F32_RECIP>
+__global__ __launch_bounds__(kRqWideThreads) void rotate_quant_wide_kernel(const uint16_t* __restrict__ x,
+                                                                          int64_t ldx, int8_t* __restrict__ q,
+                                                                          int64_t ldq, float* __restrict__ s, int K,
+                                                                          int log4g) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  double* rowbuf = reinterpret_cast<double*>(smem);
+  float* maxes = reinterpret_cast<float*>(smem + 8 * (size_t)K);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = blockIdx.x;
+  const uint16_t* xrow = x + row * ldx;
+
+  for (int p = t; p < K / 16; p += kRqWideThreads) {
+    const uint4 a = *reinterpret_cast<const uint4*>(xrow + 16 * p);
+    const uint4 b = *reinterpret_cast<const uint4*>(xrow + 16 * p + 8);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    double v[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[2 * i] = (double)bf16_lo(w[i]);
+      v[2 * i + 1] = (double)bf16_hi(w[i]);
+    }
+    h4_stage<1>(v);
+    h4_stage<4>(v);
+    double2* dst = reinterpret_cast<double2*>(rowbuf + 16 * p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = make_double2(v[2 * i], v[2 * i + 1]);
+  }
+  __syncthreads();
+  for (int d = 2; d < log4g; ++d) {
+    const int sh = 2 * d, S = 1 << sh;
+    for (int qd = t; qd < K / 4; qd += kRqWideThreads) {
+      const int i = ((qd >> sh) << (sh + 2)) | (qd & (S - 1));
+      double a = rowbuf[i], b = rowbuf[i + S], c = rowbuf[i + 2 * S], e = rowbuf[i + 3 * S];
+      h4(a, b, c, e);
+      rowbuf[i] = a;
+      rowbuf[i + S] = b;
+      rowbuf[i + 2 * S] = c;
+      rowbuf[i + 3 * S] = e;
+    }
+    __syncthreads();
+  }
+
+  auto rounded = [](double v) { return F32_RECIP ? (float)v : round_f64_to_bf16_value(v); };
+  float amax = 0.0f;
+  for (int e = t; e < K; e += kRqWideThreads) amax = fmaxf(amax, fabsf(rounded(rowbuf[e])));
+  amax = wave_max(amax);
+  if (lane == 0) maxes[wave] = amax;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(maxes[0], maxes[1]), fmaxf(maxes[2], maxes[3]));
+  const RowScale rs = row_scale_n(m, log4g);
+  const float inv_n = ldexpf(1.0f / rs.sx, -log4g);  // the reciprocal arithmetic's factor (F32_RECIP)
+  if (t == 0) s[row] = rs.sx;
+
+  // Four consecutive codes per thread, one 4-byte store.
+  int8_t* qrow = q + row * ldq;
+  for (int c = t; c < K / 4; c += kRqWideThreads) {
+    const double2 lo = *reinterpret_cast<const double2*>(rowbuf + 4 * c);
+    const double2 hi = *reinterpret_cast<const double2*>(rowbuf + 4 * c + 2);
+    const double v[4] = {lo.x, lo.y, hi.x, hi.y};
+    uint32_t code[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float f = rounded(v[i]);
+      code[i] = __float_as_uint((F32_RECIP ? f * inv_n : quotient(f, rs.d, rs.inv)) + kRoundMagic);
+    }
+    const uint32_t word = __builtin_amdgcn_perm(code[1], code[0], 0x0c0c0400u) |
+                          __builtin_amdgcn_perm(code[3], code[2], 0x04000c0cu);
+    *reinterpret_cast<uint32_t*>(qrow + 4 * c) = word;
+  }
+}
+
 template __global__ void rotate_quant_f32_recip_kernel<1>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t,
                                                           int);
 template __global__ void rotate_quant_f32_recip_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t,
@@ -504,6 +595,9 @@ template __global__ void rotate_quant_f32_recip_kernel<3>(const uint16_t*, int64
                                                           int);
 template __global__ void rotate_quant_f32_recip_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t,
                                                           int);
+
+template __global__ void rotate_quant_wide_kernel<false>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int, int);
+template __global__ void rotate_quant_wide_kernel<true>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int, int);
 
 #define HF_RQ_REG(L, T)                                                                                            \
   template __global__ void rotate_quant_reg_kernel<L, T>(const uint16_t*, int64_t, int8_t*, int64_t, float*,       \

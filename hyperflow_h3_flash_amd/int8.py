@@ -104,8 +104,8 @@ def hadamard_factors(group: int) -> tuple[int, int] | None:
     return ga, group // ga
 
 
-#: Groups the device rotation implements (powers of 4 up to 256 that divide K).
-DEVICE_GROUPS = (4, 16, 64, 256)
+#: Groups the device rotation implements (powers of 4 up to 16384 that divide K; from 1024 on, K <= 20472).
+DEVICE_GROUPS = (4, 16, 64, 256, 1024, 4096, 16384)
 
 
 def _check_group(group: int) -> None:

@@ -32,7 +32,7 @@ extern "C" {
 
 #define HF_OK 0
 #define HF_ERR_ARGUMENT (-1)  /* null pointer, negative size, stride smaller than the row */
-#define HF_ERR_GROUP (-2)     /* group is not 4, 16, 64 or 256, or does not divide K */
+#define HF_ERR_GROUP (-2)     /* group is not a power of 4 from 4 to 16384, or does not divide K */
 #define HF_ERR_ALIGNMENT (-3) /* a pointer or stride breaks the 16-byte vector-access rules below */
 #define HF_ERR_LAUNCH (-4)    /* the HIP launch failed (hipGetLastError) */
 #define HF_ERR_SIZE (-5)      /* a size exceeds what the kernels index (see each function) */
@@ -52,8 +52,8 @@ const char* hf_strerror(int status);
  *   sx[m] = max(max_k |xr[m, k]|, 1e-12) / 127                                    (int8.py:177)
  *   q[m, k] = clamp(rint(xr[m, k] / sx[m]), -127, 127)                             (int8.py:178)
  * x: bf16 [M, ldx]; q: int8 [M, ldq]; sx: fp32 [M].
- * Requires: group in {4, 16, 64, 256} dividing K; K % 16 == 0; x and q 16-byte aligned; ldx % 8 == 0;
- * ldq % 16 == 0; K <= 77312.
+ * Requires: group a power of 4 from 4 to 16384 dividing K; K % 16 == 0; x and q 16-byte aligned; ldx % 8 == 0;
+ * ldq % 16 == 0; K <= 77312, and K <= 20472 for groups of 1024 and more (a row's fp64 sums are held in LDS).
  */
 int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int64_t K,
                     int32_t group, hf_stream_t stream);
@@ -67,8 +67,9 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
  *                          sx[m] = max(max_k |xr[m, k]|, 1e-12) / 127,  inv = 1 / sx[m]   (fp32)
  *                          q[m, k] = clamp(rint(fp32(xr[m, k] * inv)), -127, 127)
  *                        Two passes over each row (the absmax, then the codes), as the reference's kernels do.
- * Same operand rules as hf_rotate_quant (any K below 2^30 for HF_ROTATE_F32_RECIP); any other arithmetic value is
- * HF_ERR_ARGUMENT. Replaces `rotate_quant(x2, group)` (int8.py:326-344) under the reference's CUDA arithmetic.
+ * Same operand rules as hf_rotate_quant (any K below 2^30 for HF_ROTATE_F32_RECIP with groups up to 256); any
+ * other arithmetic value is HF_ERR_ARGUMENT. Replaces `rotate_quant(x2, group)` (int8.py:326-344) under the
+ * reference's CUDA arithmetic.
  */
 #define HF_ROTATE_BF16_DIV 0
 #define HF_ROTATE_F32_RECIP 1

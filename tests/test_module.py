@@ -180,6 +180,6 @@ def test_device_groups_are_checked():
     with pytest.raises(ValueError, match="power of 4"):
         int8_mod._check_group(128)
     with pytest.raises(ValueError, match="not supported"):
-        int8_mod._check_group(1024)
-    for g in (4, 16, 64, 256):
+        int8_mod._check_group(65536)
+    for g in (4, 16, 64, 256, 1024, 4096, 16384):
         int8_mod._check_group(g)

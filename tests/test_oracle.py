@@ -85,6 +85,38 @@ def test_rotation_is_the_exact_sum_rounded_once(oracle_lib, group):
             assert fraction_to_bf16(exact) == int(got[r, j]), (r, j)
 
 
+def _exact_rotation_ints(xv: np.ndarray, group: int, signs: np.ndarray) -> list[Fraction]:
+    """The exact sums of one bf16 row against the +-1 signs of the regular Hadamard, in Python integers (an integer
+    dot product, not a butterfly), scaled back by the row's smallest power of two and the 2^-n normalisation."""
+    m, e = np.frexp(xv.astype(np.float64))  # xv = m * 2^e, m with at most 8 significant bits
+    mant = np.round(m * 256).astype(np.int64)
+    nz = mant != 0
+    e_min = int(e[nz].min()) - 8 if nz.any() else 0
+    ints = np.array([int(v) << int(ei - 8 - e_min) if v else 0 for v, ei in zip(mant, e)], dtype=object)
+    n = (group.bit_length() - 1) // 2
+    sums = ints.dot(signs.astype(object))
+    return [Fraction(int(t)) * Fraction(2) ** (e_min - n) for t in sums]
+
+
+@pytest.mark.parametrize("group,rows", [(256, 3), (1024, 2), (4096, 1)])
+def test_rotation_large_groups_exact_integer_sums(oracle_lib, group, rows):
+    """Groups that span whole 1024-element tiles: the exact sums as integer dot products (any magnitude: Python
+    integers), one row spanning ~250 binades (the oracle's wide accumulator) and narrow rows (its float64 path)."""
+    rng = np.random.default_rng(group + 7)
+    data = [np.exp2(rng.integers(-120, 120, size=group).astype(np.float64)) * rng.choice([-1, 1], size=group)]
+    for _ in range(rows - 1):
+        data.append(rng.standard_normal(group) * 4.0)
+    x = _bits(np.array(data, dtype=np.float64).astype(np.float32))
+    signs = np.sign(oracle_lib.regular_hadamard(group)).astype(np.int64)
+    got = oracle_lib.rotate(x, group)
+    got_exact = oracle_lib.rotate(x, group, force_exact=True)
+    for r in range(x.shape[0]):
+        exact = _exact_rotation_ints(oracle_lib.bf16_to_f32(x[r]), group, signs)
+        want = np.array([fraction_to_bf16(v) for v in exact], dtype=np.uint16)
+        np.testing.assert_array_equal(got_exact[r], want)
+        np.testing.assert_array_equal(got[r], want)
+
+
 def test_rotation_rounds_ties_to_even(oracle_lib):
     # G=4: out_0 = (x0 + x1 + x2 - x3) / 2. (1 + 2^-8)/2 = 0.5 + 2^-9 is the midpoint between 0.5 (even) and
     # 0.5 + 2^-8; (1 + 3*2^-8)/2 is the midpoint between 0.5 + 2^-8 (odd) and 0.5 + 2^-7 (even).
