@@ -413,12 +413,16 @@ void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t
   const int t0 = part * TPW;
 
   // held[i] first receives tile i's raw pencil in its first 8 words (all of this wave's loads in flight at once),
-  // then the tile's 16 rounded values.
+  // then the tile's 16 rounded values. The loads go through a buffer descriptor that covers the row's valid bytes
+  // (none for a row past the matrix): a pencil at or past K reads as zeros without a branch, so every load is issued
+  // unconditionally in order and tile i waits only for its own two loads, not for the whole row's.
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xrow, 2u * (uint32_t)kvalid);
   float held[TPW][16];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
-    uint4 a, b;
-    load_pencil(xrow, (t0 + i) * kRqTile + lane * 16, kvalid, a, b);
+    const int off = 2 * ((t0 + i) * kRqTile + lane * 16);
+    const v4u a = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+    const v4u b = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16, 0, 0);
     const uint32_t raw[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) held[i][j] = __uint_as_float(raw[j]);
