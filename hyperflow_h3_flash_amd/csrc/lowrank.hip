@@ -221,7 +221,7 @@ __device__ __forceinline__ void lane_fold(float (&a)[kLrRowRanks], int lane) {
 __device__ __forceinline__ void lowrank_row_ranks(const uint16_t* __restrict__ xrow,
                                                   const uint16_t* __restrict__ down, int64_t ld_down,
                                                   uint16_t* __restrict__ urow, int K, int r, int j0, float* sums) {
-  const int lane = threadIdx.x & 63, t = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, t = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
   // Lanes past K (in the last wave) load in-range elements and contribute zero; ranks past r load row r - 1 and are
   // not stored. No load is predicated, so all of them issue at once.
   const bool live = t * 1024 + lane * 16 < K;

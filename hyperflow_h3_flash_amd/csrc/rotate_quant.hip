@@ -26,7 +26,7 @@ namespace hf {
 constexpr int kRqTile = 1024;                            // elements per wave step (64 lanes x 16)
 constexpr int kRqStride = 18;                            // doubles per pencil in the transpose scratch (16 + pad)
 constexpr int kRqScratchBytes = 64 * kRqStride * 8;      // 9216 bytes per wave
-constexpr int kRqRegMaxTpw = 5;  // tiles per wave of the register-resident kernel (three waves per SIMD at five)
+constexpr int kRqRegMaxTpw = 5;  // tiles per wave of the register-resident kernel (four waves per SIMD at five)
 
 __device__ __forceinline__ void h4(double& a, double& b, double& c, double& d) {
   double s = (a + b) + (c + d);
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(256) void rotate_quant_kernel(const uint16_t* __res
                                                            float* __restrict__ s, int64_t M, int K) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar addressing
   const int waves = blockDim.x >> 6;
   unsigned char* mine = smem + (size_t)wave * (kRqScratchBytes + 2 * (size_t)K);
   double* scratch = reinterpret_cast<double*>(mine);
@@ -303,7 +303,7 @@ __device__ __forceinline__ void rotate_quant_row(const uint16_t* __restrict__ x,
                                                  int64_t ldq, float* __restrict__ s, int K, int64_t row,
                                                  unsigned char* smem) {
   const int lane = threadIdx.x & 63;
-  const int t = threadIdx.x >> 6;  // this wave's tile
+  const int t = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's tile (uniform)
   const int ntiles = blockDim.x >> 6;
   double* scratch = reinterpret_cast<double*>(smem + (size_t)t * kRqScratchBytes);
   uint16_t* rowbuf = reinterpret_cast<uint16_t*>(smem + (size_t)ntiles * kRqScratchBytes);
@@ -393,15 +393,15 @@ __device__ __forceinline__ void quantize_store_tile(const float (&f)[16], const 
 
 size_t rotate_quant_reg_lds_bytes(int waves) { return (size_t)waves * kRqScratchBytes + 16; }
 
-// Five tiles per wave held as fp32 (80 VGPRs; ~136 in all) leave three waves per SIMD when the compiler is held to
-// it. Holding them as packed bf16 pairs (four waves per SIMD) cost a pack and an unpack per value: 3-5 % slower.
+// Five tiles per wave held as fp32 (80 VGPRs; 118 in all with the wave index and the row descriptor in scalar
+// registers) leave four waves per SIMD.
 template <int LOG4G, int TPW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TPW == kRqRegMaxTpw ? 3 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TPW == kRqRegMaxTpw ? 4 : 1)))
 void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
                              float* __restrict__ s, int64_t M, int K, int wpr) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar addressing
   const int nwaves = blockDim.x >> 6;
   double* scratch = reinterpret_cast<double*>(smem + (size_t)wave * kRqScratchBytes);
   float* maxes = reinterpret_cast<float*>(smem + (size_t)nwaves * kRqScratchBytes);
@@ -472,7 +472,7 @@ __global__ __launch_bounds__(256) void rotate_quant_f32_recip_kernel(const uint1
                                                                      float* __restrict__ s, int64_t M, int K) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar addressing
   const int waves = blockDim.x >> 6;
   double* scratch = reinterpret_cast<double*>(smem + (size_t)wave * kRqScratchBytes);
   unsigned char* stage = reinterpret_cast<unsigned char*>(scratch);
@@ -527,7 +527,7 @@ __global__ __launch_bounds__(kRqWideThreads) void rotate_quant_wide_kernel(const
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   double* rowbuf = reinterpret_cast<double*>(smem);
   float* maxes = reinterpret_cast<float*>(smem + 8 * (size_t)K);
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int64_t row = blockIdx.x;
   const uint16_t* xrow = x + row * ldx;
 
