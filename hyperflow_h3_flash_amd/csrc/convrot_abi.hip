@@ -696,9 +696,13 @@ namespace {
 
 // The rotation (bf16_div arithmetic) and the low-rank down projection of a few rows in one launch
 // (rotate_lowrank_row_kernel): the argument rules of hf_rotate_quant and hf_lowrank_down together. Used when both
-// would run their row kernels.
+// would run their row kernels and the rows are few: the low-rank workgroups take the rotation's dynamic LDS (about
+// 11 KiB per 1024-element tile), so with more rows they fit fewer per CU than alone. Layer A/B (HIP graph, N=5120,
+// rank 64): one launch ahead by 1-5 us up to 128 rows at every K and up to 192 rows at 7 or fewer tiles; behind by
+// 1-8 us at 256-384 rows with K=5120 or K=14336.
 bool rotate_lowrank_by_rows(int64_t M, int64_t K) {
-  return lowrank_by_rows(M, K) && M <= kRowKernelMaxRows && (K + hf::kRqTile - 1) / hf::kRqTile <= 14;
+  const int64_t ntiles = (K + hf::kRqTile - 1) / hf::kRqTile;
+  return lowrank_by_rows(M, K) && M <= kRowKernelMaxRows && ntiles <= 14 && (M <= 128 || (M <= 192 && ntiles <= 7));
 }
 
 int rotate_lowrank_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, const uint16_t* down,
