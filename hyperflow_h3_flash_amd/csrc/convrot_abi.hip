@@ -61,6 +61,8 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<4>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<5>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<1>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<2>),
@@ -69,6 +71,8 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<4>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_row_kernel<5>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_lowrank_row_kernel<1>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_lowrank_row_kernel<2>),
@@ -76,6 +80,8 @@ void allow_large_lds() {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_lowrank_row_kernel<3>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_lowrank_row_kernel<4>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_lowrank_row_kernel<5>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
 #define HF_LR_ATTR(RB, NW)                                                                                \
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_kernel<RB, NW>),             \
@@ -103,7 +109,7 @@ void allow_large_lds() {
   });
 }
 
-// Groups of 1024 and more: rotate_quant_wide_kernel, one workgroup per row with the row's fp64 sums in LDS
+// Groups of 4096 and more: rotate_quant_wide_kernel, one workgroup per row with the row's fp64 sums in LDS
 // (K * 8 bytes, so K <= 20472). The caller has checked the group, the alignment and M > 0.
 int launch_rotate_wide(bool f32_recip, int lg, const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx,
                        int64_t M, int64_t K, hipStream_t s) {
@@ -131,6 +137,7 @@ int launch_rotate_reg(int lg, int tpw, dim3 grid, dim3 block, size_t lds, hipStr
   HF_RQ_CASES(2)
   HF_RQ_CASES(3)
   HF_RQ_CASES(4)
+  HF_RQ_CASES(5)
 #undef HF_RQ_CASES
 #undef HF_RQ_CASE
   return HF_ERR_ARGUMENT;
@@ -532,7 +539,7 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
   const int lg = log4_of(group);
   if (lg < 0 || K % group) return HF_ERR_GROUP;
   if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16)) return HF_ERR_ALIGNMENT;
-  if (lg >= 5) return launch_rotate_wide(false, lg, x, ldx, q, ldq, sx, M, K, static_cast<hipStream_t>(stream));
+  if (lg >= 6) return launch_rotate_wide(false, lg, x, ldx, q, ldq, sx, M, K, static_cast<hipStream_t>(stream));
   int waves = 4;
   while (waves > 0 && hf::rotate_quant_lds_bytes(waves, (int)std::min<int64_t>(K, 1 << 30)) > (size_t)kMaxLds)
     waves >>= 1;
@@ -551,7 +558,8 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
       case 1: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<1>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
       case 2: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<2>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
       case 3: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<3>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
-      default: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<4>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
+      case 4: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<4>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
+      default: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<5>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
     }
     return launch_status();
   }
@@ -573,7 +581,8 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
     case 1: hipLaunchKernelGGL(hf::rotate_quant_kernel<1>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
     case 2: hipLaunchKernelGGL(hf::rotate_quant_kernel<2>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
     case 3: hipLaunchKernelGGL(hf::rotate_quant_kernel<3>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
-    default: hipLaunchKernelGGL(hf::rotate_quant_kernel<4>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    case 4: hipLaunchKernelGGL(hf::rotate_quant_kernel<4>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    default: hipLaunchKernelGGL(hf::rotate_quant_kernel<5>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
   }
   return launch_status();
 }
@@ -590,7 +599,7 @@ int hf_rotate_quant_ex(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, f
   if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16)) return HF_ERR_ALIGNMENT;
   if (K >= (int64_t(1) << 30)) return HF_ERR_SIZE;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (lg >= 5) return launch_rotate_wide(true, lg, x, ldx, q, ldq, sx, M, K, s);
+  if (lg >= 6) return launch_rotate_wide(true, lg, x, ldx, q, ldq, sx, M, K, s);
   constexpr int waves = 4;
   const size_t lds = hf::rotate_quant_f32_recip_lds_bytes(waves);
   const unsigned blocks = (unsigned)std::min<int64_t>((M + waves - 1) / waves, int64_t(1) << 30);
@@ -598,7 +607,8 @@ int hf_rotate_quant_ex(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, f
     case 1: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<1>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
     case 2: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<2>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
     case 3: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<3>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
-    default: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<4>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    case 4: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<4>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    default: hipLaunchKernelGGL(hf::rotate_quant_f32_recip_kernel<5>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
   }
   return launch_status();
 }
@@ -712,7 +722,7 @@ int rotate_lowrank_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, 
   if (M == 0) return HF_OK;
   if (!x || !q || !sx || !down || !u) return HF_ERR_ARGUMENT;
   const int lg = log4_of(group);
-  if (lg < 0 || lg > 4 || K % group) return HF_ERR_GROUP;
+  if (lg < 0 || lg > 5 || K % group) return HF_ERR_GROUP;
   if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16) || !aligned(down, 16) ||
       (ld_down % 8) || !aligned(u, 8))
     return HF_ERR_ALIGNMENT;
@@ -730,7 +740,8 @@ int rotate_lowrank_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, 
     case 1: HF_RLR(1); break;
     case 2: HF_RLR(2); break;
     case 3: HF_RLR(3); break;
-    default: HF_RLR(4); break;
+    case 4: HF_RLR(4); break;
+    default: HF_RLR(5); break;
   }
 #undef HF_RLR
   return launch_status();
@@ -754,7 +765,7 @@ int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, i
   if (M < 0 || N < 0 || K <= 0 || r < 0) return HF_ERR_ARGUMENT;
   if (M == 0 || N == 0) return HF_OK;
   int st = HF_OK;
-  if (!quantized && r > 0 && arithmetic == HF_ROTATE_BF16_DIV && group <= 256 && rotate_lowrank_by_rows(M, K)) {
+  if (!quantized && r > 0 && arithmetic == HF_ROTATE_BF16_DIV && group <= 1024 && rotate_lowrank_by_rows(M, K)) {
     st = rotate_lowrank_rows(x, ldx, q, K, sx, down, ld_down, u, r, M, K, r, group, stream);
     if (st != HF_OK) return st;
   } else {

@@ -62,12 +62,20 @@ size_t rotate_quant_lds_bytes(int waves, int K) { return (size_t)waves * (kRqScr
 //   LOG4G <= 2: 16 lane + 2i + h                                   (natural order)
 //   LOG4G == 3: lane = 4 gi + cq: 64 gi + 16 (i / 2) + 4 cq + 2 (i % 2) + h
 //   LOG4G == 4: lane = 16 gi + b: 256 gi + 16 (2i + h) + b
+//   LOG4G == 5: lane = 16 A + b, value v = 2i + h = 4k + g: 256 g + 16 (4A + k) + b   (the tile is one group)
 template <int LOG4G>
 __device__ __forceinline__ int held_offset(int lane, int i, int h) {
   if constexpr (LOG4G <= 2) return 16 * lane + 2 * i + h;
   if constexpr (LOG4G == 3) return 64 * (lane >> 2) + 16 * (i >> 1) + 4 * (lane & 3) + 2 * (i & 1) + h;
-  return 256 * (lane >> 4) + 16 * (2 * i + h) + (lane & 15);
+  if constexpr (LOG4G == 4) return 256 * (lane >> 4) + 16 * (2 * i + h) + (lane & 15);
+  const int v = 2 * i + h;
+  return 256 * (v & 3) + 16 * (4 * (lane >> 4) + (v >> 2)) + (lane & 15);
 }
+
+// Rows of the second transpose (LOG4G == 5): 17 doubles apart, so the four 16-lane groups of a read land on
+// distinct banks.
+constexpr int kRqStride2 = 17;
+static_assert(64 * kRqStride2 <= 64 * kRqStride, "the second transpose fits the wave's scratch");
 
 // Rotates one 1024-element tile (this lane's 16 consecutive inputs 16 lane .. 16 lane + 15 in cur0, cur1): v[2i + h]
 // receives the exact unnormalised sum of value 2i + h of the layout of held_offset. `scratch` is the wave's fp64
@@ -92,13 +100,27 @@ __device__ __forceinline__ void rotate_tile_f64(uint4 cur0, uint4 cur1, int lane
       *reinterpret_cast<double2*>(scratch + lane * kRqStride + 2 * i) = pr;
     }
     wave_lds_sync();
-    if constexpr (LOG4G == 4) {
+    if constexpr (LOG4G >= 4) {
       // lane = 16*gi + b; v[a] = pencil (16*gi + a), column b
       const int gi = lane >> 4, b = lane & 15;
 #pragma unroll
       for (int a = 0; a < 16; ++a) v[a] = scratch[(16 * gi + a) * kRqStride + b];
       h4_stage<1>(v);
       h4_stage<4>(v);
+      if constexpr (LOG4G == 5) {
+        // Digit 4 is gi (lane bits 4-5): a second pass through LDS gives lane (A, b) the values of a = 4A + k for
+        // every gi, v[4k + gi], and one more radix-4 stage runs along gi.
+        wave_lds_sync();  // every lane has read the first transpose
+#pragma unroll
+        for (int a = 0; a < 16; ++a) scratch[(16 * gi + a) * kRqStride2 + b] = v[a];
+        wave_lds_sync();
+        const int A = lane >> 4;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) v[4 * k + g] = scratch[(16 * g + 4 * A + k) * kRqStride2 + b];
+        h4_stage<1>(v);
+      }
     } else {
       // lane = 4*gi + cq; v[4a + cc] = pencil (4*gi + a), column 4*cq + cc
       const int gi = lane >> 2, cq = lane & 3;
@@ -394,9 +416,9 @@ __device__ __forceinline__ void quantize_store_tile(const float (&f)[16], const 
 size_t rotate_quant_reg_lds_bytes(int waves) { return (size_t)waves * kRqScratchBytes + 16; }
 
 // Five tiles per wave held as fp32 (80 VGPRs; 118 in all with the wave index and the row descriptor in scalar
-// registers) leave four waves per SIMD.
+// registers) leave four waves per SIMD (three with the 1024 group's second transpose).
 template <int LOG4G, int TPW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TPW == kRqRegMaxTpw ? 4 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TPW == kRqRegMaxTpw ? (LOG4G == 5 ? 3 : 4) : 1)))
 void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
                              float* __restrict__ s, int64_t M, int K, int wpr) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -599,6 +621,8 @@ template __global__ void rotate_quant_f32_recip_kernel<3>(const uint16_t*, int64
                                                           int);
 template __global__ void rotate_quant_f32_recip_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t,
                                                           int);
+template __global__ void rotate_quant_f32_recip_kernel<5>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t,
+                                                          int);
 
 template __global__ void rotate_quant_wide_kernel<false>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int, int);
 template __global__ void rotate_quant_wide_kernel<true>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int, int);
@@ -611,6 +635,7 @@ HF_RQ_REG_ALL(1)
 HF_RQ_REG_ALL(2)
 HF_RQ_REG_ALL(3)
 HF_RQ_REG_ALL(4)
+HF_RQ_REG_ALL(5)
 #undef HF_RQ_REG_ALL
 #undef HF_RQ_REG
 
@@ -618,10 +643,12 @@ template __global__ void rotate_quant_kernel<1>(const uint16_t*, int64_t, int8_t
 template __global__ void rotate_quant_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
 template __global__ void rotate_quant_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
 template __global__ void rotate_quant_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
+template __global__ void rotate_quant_kernel<5>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
 template __global__ void rotate_quant_row_kernel<1>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
 template __global__ void rotate_quant_row_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
 template __global__ void rotate_quant_row_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
 template __global__ void rotate_quant_row_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
+template __global__ void rotate_quant_row_kernel<5>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
 #define HF_RQ_LR_ROW(G)                                                                                             \
   template __global__ void rotate_lowrank_row_kernel<G>(const uint16_t*, int64_t, int8_t*, int64_t, float*,         \
                                                         const uint16_t*, int64_t, uint16_t*, int64_t, int, int, int, \
@@ -630,6 +657,7 @@ HF_RQ_LR_ROW(1)
 HF_RQ_LR_ROW(2)
 HF_RQ_LR_ROW(3)
 HF_RQ_LR_ROW(4)
+HF_RQ_LR_ROW(5)
 #undef HF_RQ_LR_ROW
 
 }  // namespace hf

@@ -104,7 +104,7 @@ def hadamard_factors(group: int) -> tuple[int, int] | None:
     return ga, group // ga
 
 
-#: Groups the device rotation implements (powers of 4 up to 16384 that divide K; from 1024 on, K <= 20472).
+#: Groups the device rotation implements (powers of 4 up to 16384 that divide K; from 4096 on, K <= 20472).
 DEVICE_GROUPS = (4, 16, 64, 256, 1024, 4096, 16384)
 
 

@@ -53,7 +53,7 @@ const char* hf_strerror(int status);
  *   q[m, k] = clamp(rint(xr[m, k] / sx[m]), -127, 127)                             (int8.py:178)
  * x: bf16 [M, ldx]; q: int8 [M, ldq]; sx: fp32 [M].
  * Requires: group a power of 4 from 4 to 16384 dividing K; K % 16 == 0; x and q 16-byte aligned; ldx % 8 == 0;
- * ldq % 16 == 0; K <= 77312, and K <= 20472 for groups of 1024 and more (a row's fp64 sums are held in LDS).
+ * ldq % 16 == 0; K <= 77312, and K <= 20472 for groups of 4096 and more (a row's fp64 sums are held in LDS).
  */
 int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int64_t K,
                     int32_t group, hf_stream_t stream);
