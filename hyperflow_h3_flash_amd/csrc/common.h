@@ -137,6 +137,13 @@ __device__ __forceinline__ int64_t partial_block_offset(int bm, int bn, int nbn)
   return ((int64_t)bm * nbn + bn) * 1024;
 }
 
+// A 16-byte store of a result nothing in the same kernel reads again (a GEMM's output tile), with the non-temporal
+// hint: the line is written without being kept in the XCD's L2. A GEMM writing its output through the normal
+// policy fills each 4 MiB L2 with output lines and evicts the operand panels the XCD's concurrent tiles share,
+// which are then fetched again from the Infinity Cache (measured at M=32768, K=5120, N=15360: 2435 -> 2125 us,
+// same box).
+__device__ __forceinline__ void store_stream(v4i* dst, v4i v) { __builtin_nontemporal_store(v, dst); }
+
 // Buffer resource for raw (stride 0) buffer loads: offsets at or beyond `bytes` read as zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);

@@ -460,10 +460,10 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
             int32_t* dst = out + (int64_t)m * a.ldo + n;
             const v16i& c = acc[ib][jb];
             if (full) {
-              *reinterpret_cast<v4i*>(dst) = (v4i){c[4 * gq], c[4 * gq + 1], c[4 * gq + 2], c[4 * gq + 3]};
+              store_stream(reinterpret_cast<v4i*>(dst), (v4i){c[4 * gq], c[4 * gq + 1], c[4 * gq + 2], c[4 * gq + 3]});
             } else if (m < a.M) {
               if (a.out_vec16 && n + 4 <= a.N) {
-                *reinterpret_cast<v4i*>(dst) = (v4i){c[4 * gq], c[4 * gq + 1], c[4 * gq + 2], c[4 * gq + 3]};
+                store_stream(reinterpret_cast<v4i*>(dst), (v4i){c[4 * gq], c[4 * gq + 1], c[4 * gq + 2], c[4 * gq + 3]});
               } else {
                 for (int e = 0; e < 4; ++e)
                   if (n + e < a.N) dst[e] = c[4 * gq + e];
@@ -642,10 +642,10 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
           const int n = no0 + 8 * ch;
           uint16_t* dst = out + (int64_t)m * a.ldo + n;
           if (full) {
-            *reinterpret_cast<v4i*>(dst) = val;
+            store_stream(reinterpret_cast<v4i*>(dst), val);
           } else if (m < a.M) {
             if (a.out_vec16 && n + 8 <= n_out) {
-              *reinterpret_cast<v4i*>(dst) = val;
+              store_stream(reinterpret_cast<v4i*>(dst), val);
             } else {
               for (int e = 0; e < 8; ++e)
                 if (n + e < n_out) dst[e] = (uint16_t)((uint32_t)val[e >> 1] >> (16 * (e & 1)));
@@ -680,10 +680,10 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
             const int n = n0 + wn * WN + 32 * pb + 8 * ch;
             uint16_t* dst = out + (int64_t)m * a.ldo + n;
             if (full) {
-              *reinterpret_cast<v4i*>(dst) = val;
+              store_stream(reinterpret_cast<v4i*>(dst), val);
             } else if (m < a.M) {
               if (a.out_vec16 && n + 8 <= a.N) {
-                *reinterpret_cast<v4i*>(dst) = val;
+                store_stream(reinterpret_cast<v4i*>(dst), val);
               } else {
                 for (int e = 0; e < 8; ++e)
                   if (n + e < a.N) dst[e] = (uint16_t)((uint32_t)val[e >> 1] >> (16 * (e & 1)));
