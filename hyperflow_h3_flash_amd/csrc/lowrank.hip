@@ -39,7 +39,10 @@ __device__ __forceinline__ int lr_swizzle(int row, int c) { return swizzle128(ro
 
 // One wave's share of a stage: `count` loads of 1 KiB (8 rows x 128 bytes) starting at LDS block `first_blk`.
 // Rows at or past `rows_valid`, and chunks at or past K, read as zero (offset `oob` is past the descriptor).
-template <int COUNT>
+// CPOL is the loads' cache policy: kCpolStream for x, which this pass reads last in a layer (after the rotation),
+// so its 2 bytes per element are not kept in the Infinity Cache over the codes the GEMM reads next.
+constexpr int kCpolStream = 2;  // the nt (non-temporal) bit
+template <int COUNT, int CPOL = 0>
 __device__ __forceinline__ void lr_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t oob, uint32_t ld_bytes, int rows_valid,
                                         int k0, int K, unsigned char HF_LDS* dst, int first_blk, int lane) {
 #pragma unroll
@@ -49,7 +52,7 @@ __device__ __forceinline__ void lr_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t oo
     const int c = lr_swizzle(row, lane & 7);
     const int k = k0 + c * 8;
     const uint32_t voff = ((row < rows_valid) & (k < K)) ? (uint32_t)row * ld_bytes + (uint32_t)k * 2u : oob;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + blk * 1024), 16, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (void HF_LDS*)(dst + blk * 1024), 16, voff, 0, 0, CPOL);
   }
 }
 
@@ -88,7 +91,7 @@ __global__ __launch_bounds__(64 * NW, 1) void lowrank_down_kernel(const uint16_t
   // the kStages - 2 later stages in flight.
   auto issue = [&](int t) {
     unsigned char HF_LDS* st = smem + (t % kStages) * kStageBytes;
-    lr_load<4>(rx, bytes_x, ldx_bytes, rows_m, t * kLrStageK, k_len, st, wave * 4, lane);
+    lr_load<4, kCpolStream>(rx, bytes_x, ldx_bytes, rows_m, t * kLrStageK, k_len, st, wave * 4, lane);
     lr_load<2>(rd, bytes_d, ldd_bytes, r, t * kLrStageK, k_len, st + kXBytes, (wave % 4) * 2, lane);
   };
 
