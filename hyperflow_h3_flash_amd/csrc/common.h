@@ -138,10 +138,11 @@ __device__ __forceinline__ int64_t partial_block_offset(int bm, int bn, int nbn)
 }
 
 // A 16-byte store of a result nothing in the same kernel reads again (a GEMM's output tile), with the non-temporal
-// hint: the line is written without being kept in the XCD's L2. A GEMM writing its output through the normal
-// policy fills each 4 MiB L2 with output lines and evicts the operand panels the XCD's concurrent tiles share,
-// which are then fetched again from the Infinity Cache (measured at M=32768, K=5120, N=15360: 2435 -> 2125 us,
-// same box).
+// hint. Written with the normal policy, a GEMM's output (1 GB at M=32768, N=15360) is allocated in the 256 MiB
+// Infinity Cache and displaces the operands (codes and weight, ~250 MB) whose panels every XCD's L2 fetches again
+// each round; those fetches then come from HBM. Measured at M=32768, K=5120, N=15360 with the rotation and low-rank
+// pass before it: the same number of L2 fetches, their mean latency at the L2's fabric interface ~600 -> ~490
+// cycles, MFMA busy 66 -> 69.5 % at the same clock, the layer 2413 -> 2324 us (same box).
 __device__ __forceinline__ void store_stream(v4i* dst, v4i v) { __builtin_nontemporal_store(v, dst); }
 
 // Buffer resource for raw (stride 0) buffer loads: offsets at or beyond `bytes` read as zero.
