@@ -9,6 +9,7 @@
 #include "rotate_quant.hip"
 #include "skinny.hip"
 #include "splitk.hip"
+#include "skinny_fused.hip"
 
 namespace {
 
@@ -53,6 +54,10 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActSwiGLU>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_fused_kernel<64, false>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::sf_lds(64));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_fused_kernel<64, true>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, hf::sf_lds(64));
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<1>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_kernel<2>),
@@ -374,6 +379,20 @@ bool use_mid_gemm(int64_t M, int64_t N, int32_t r, bool glu) {
   return 2 * tiles_m * ((N + hf::kMidBN - 1) / hf::kMidBN) >= cus;
 }
 
+#ifndef HF_SKINNY_FUSED
+#define HF_SKINNY_FUSED 1
+#endif
+
+// Whether a GEMM of at most 64 rows runs in one pass (skinny_fused_kernel): its 32-row weight slices fill between a
+// quarter of the CUs and one round of them. Each workgroup's weight stream is latency-bound (the codes take two thirds
+// of each stage), so against the split-K path (128-row slices over K chunks, partial planes and a finishing pass) it
+// wins only while the slices fit one round: M=64, N=5120 16.0 -> 14.8 us, M=16 13.9 -> 12.3 us; at N=30720 (3.75
+// rounds) 60 against 44 us, and with 128 rows (21.5 against 17.9 us) the split path stays.
+bool use_skinny_fused(int64_t M, int64_t N) {
+  const int64_t slices = (N + hf::kSfN - 1) / hf::kSfN;
+  return HF_SKINNY_FUSED && M <= 64 && 4 * slices >= device_cus() && slices <= device_cus();
+}
+
 // Rows of a many-tile GEMM that run as whole 256 x 256 tiles; the rest (the trailing tile rows) run as a separate
 // few-row GEMM, split over K. The persistent grid takes ceil(tiles / CUs) rounds; when the last round is less than
 // half full, its tiles keep a few CUs busy for a whole tile time while the others idle. Peeling off the trailing
@@ -457,6 +476,20 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
       hipLaunchKernelGGL(hf::mid_gemm_kernel<hf::kActGeluTanh>, grid, block, hf::kMidLds, s, a);
     else
       hipLaunchKernelGGL(hf::mid_gemm_kernel<hf::kActNone>, grid, block, hf::kMidLds, s, a);
+    return launch_status();
+  }
+  if (use_skinny_fused(M, N)) {
+    // At most 64 rows: one pass, 32 weight rows per workgroup with the whole K, the epilogue in the same kernel.
+    allow_large_lds();
+    const int vec = aligned(y, 8) && (ldy % 4) == 0;
+    const int gh = glu ? glu_half : 0, gf = glu ? glu_gate_first : 0;
+    const dim3 grid((unsigned)((N + hf::kSfN - 1) / hf::kSfN)), block(64 * hf::kSfWaves);
+#define HF_SF_LAUNCH(MR, GLU)                                                                                       \
+  hipLaunchKernelGGL((hf::skinny_fused_kernel<MR, GLU>), grid, block, hf::sf_lds(MR), s, q, ldq, w, ldw, sx, sw,     \
+                     r > 0 ? u : nullptr, ldu, r > 0 ? up : nullptr, ld_up, r, bias, y, ldy, (int)M, (int)N, (int)K, \
+                     vec, act, gh, gf)
+    if (glu) HF_SF_LAUNCH(64, true); else HF_SF_LAUNCH(64, false);
+#undef HF_SF_LAUNCH
     return launch_status();
   }
   const GemmPlan plan = gemm_plan(M, N, K);

@@ -122,8 +122,9 @@ int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, c
                    uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hf_stream_t stream);
 
 /*
- * hf_int8_linear with a caller-provided workspace (16-byte aligned): when the output has fewer 256 x 256 tiles than
- * the device has CUs (few rows), K is split across workgroups; their int32 partial accumulators (`ws`) are added
+ * hf_int8_linear with a caller-provided workspace (16-byte aligned): at most 64 rows whose 32-row weight slices fill
+ * between a quarter and one round of the CUs run in one pass with no workspace; otherwise, when the output has fewer
+ * 256 x 256 tiles than the device has CUs (few rows), K is split across workgroups; their int32 partial accumulators (`ws`) are added
  * exactly and the same epilogue is applied, so the result equals hf_int8_linear's bit for bit. With many tiles
  * whose last round on the CUs would be less than half full and deep K, the trailing tile rows run that way and the
  * rest as whole tiles. `hf_int8_linear_ws_bytes` gives the bytes used for these sizes (0: no split); a NULL or
