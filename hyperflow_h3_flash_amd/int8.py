@@ -109,7 +109,10 @@ DEVICE_GROUPS = (4, 16, 64, 256, 1024, 4096, 16384)
 
 
 def _check_group(group: int) -> None:
-    regular_hadamard(group)  # ValueError for a non-power of 4, as the reference raises at first use
+    # ValueError for a non-power of 4, as the reference raises at first use; decided from the number alone (building
+    # the matrix first would take 2 GiB at 16384 and 32 GiB at 65536).
+    if group < 1 or group & (group - 1) or (group.bit_length() - 1) % 2:
+        raise ValueError(f"Hadamard group {group} is not a power of 4")
     if group not in DEVICE_GROUPS:
         raise ValueError(f"Hadamard group {group} is not supported by the gfx950 kernels (supported: {DEVICE_GROUPS})")
 
