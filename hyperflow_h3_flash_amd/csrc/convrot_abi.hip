@@ -379,10 +379,6 @@ bool use_mid_gemm(int64_t M, int64_t N, int32_t r, bool glu) {
   return 2 * tiles_m * ((N + hf::kMidBN - 1) / hf::kMidBN) >= cus;
 }
 
-#ifndef HF_SKINNY_FUSED
-#define HF_SKINNY_FUSED 1
-#endif
-
 // Whether a GEMM of at most 64 rows runs in one pass (skinny_fused_kernel): its 32-row weight slices fill between a
 // quarter of the CUs and one round of them. Each workgroup's weight stream is latency-bound (the codes take two thirds
 // of each stage), so against the split-K path (128-row slices over K chunks, partial planes and a finishing pass) it
@@ -390,7 +386,7 @@ bool use_mid_gemm(int64_t M, int64_t N, int32_t r, bool glu) {
 // rounds) 60 against 44 us, and with 128 rows (21.5 against 17.9 us) the split path stays.
 bool use_skinny_fused(int64_t M, int64_t N) {
   const int64_t slices = (N + hf::kSfN - 1) / hf::kSfN;
-  return HF_SKINNY_FUSED && M <= 64 && 4 * slices >= device_cus() && slices <= device_cus();
+  return M <= 64 && 4 * slices >= device_cus() && slices <= device_cus();
 }
 
 // Rows of a many-tile GEMM that run as whole 256 x 256 tiles; the rest (the trailing tile rows) run as a separate
