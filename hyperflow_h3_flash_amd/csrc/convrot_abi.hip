@@ -34,10 +34,14 @@ int log4_of(int32_t group) {
   }
 }
 
-// Kernels that use more than 64 KiB of dynamic LDS must say so once per process.
+// Kernels that use more than 64 KiB of dynamic LDS must say so, once per device (the attribute belongs to the
+// kernel's code object on the current device); devices past the 64th set it on every call.
 void allow_large_lds() {
-  static std::once_flag once;
-  std::call_once(once, [] {
+  static std::once_flag once[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  std::once_flag spare;
+  std::call_once(dev < 64 ? once[dev] : spare, [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutI32>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutI32, hf::kActSwiGLU>),
