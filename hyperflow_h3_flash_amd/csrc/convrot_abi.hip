@@ -371,16 +371,25 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
 
 // Whether a GEMM runs as 256 x 128 tiles (mid_gemm_kernel): its 256 x 256 tiles are fewer than the CUs, it is too
 // tall for the 128-row weight slices (skinny_gemm_kernel), and the 256 x 128 tiles fill at least half the CUs, so no
-// K split (with its int32 partial planes and finishing pass) is needed. The kernel's epilogue covers rank <= 64 and
-// the tanh-GELU; gated (SwiGLU) outputs keep the split path.
-bool use_mid_gemm(int64_t M, int64_t N, int32_t r, bool glu) {
+// K split (with its int32 partial planes and finishing pass) is needed. Between a quarter and half of the CUs the
+// tiles' single round is weighed against the split path with times measured on MI355X (M=512-1024, N=2048-5120,
+// K=2048-5120, graph replays): the tiles take ~0.9 us per 128-byte K stage plus ~3 us, the split GEMM and its
+// finishing pass ~21 us plus ~0.62 us per 10^9 int8 operations (e.g. M=1024, N=K=3072: 25.5 against 31.8 us; at
+// M=512, N=4096, K=5120 the split path's 33.4 against 37.7 us). The kernel's epilogue covers rank <= 64 and the
+// tanh-GELU; gated (SwiGLU) outputs keep the split path.
+bool use_mid_gemm(int64_t M, int64_t N, int64_t K, int32_t r, bool glu) {
   if (glu || r > 64) return false;
   const int64_t cus = device_cus();
   const int64_t tiles_m = (M + hf::GBM - 1) / hf::GBM;
   if (tiles_m * ((N + hf::GBN - 1) / hf::GBN) >= cus) return false;
   const int64_t ntiles = (N + hf::kSkinnyN - 1) / hf::kSkinnyN;
   if (M <= 128 || (M <= hf::kSkinnyMaxM && 2 * ntiles <= cus)) return false;
-  return 2 * tiles_m * ((N + hf::kMidBN - 1) / hf::kMidBN) >= cus;
+  const int64_t tiles = tiles_m * ((N + hf::kMidBN - 1) / hf::kMidBN);
+  if (2 * tiles >= cus) return true;
+  if (4 * tiles < cus) return false;
+  const double stages = (double)((K + hf::kMidBK - 1) / hf::kMidBK);
+  const double t_tiles = 0.9 * stages + 3.0, t_split = 21.0 + 0.62e-9 * 2.0 * (double)M * (double)N * (double)K;
+  return t_tiles < t_split;
 }
 
 // Whether a GEMM of at most 64 rows runs in one pass (skinny_fused_kernel): its 32-row weight slices fill between a
@@ -462,7 +471,7 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
     return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, m_main, N, K, nullptr, 0,
                             stream, act_code);
   }
-  if (use_mid_gemm(M, N, r, glu)) {
+  if (use_mid_gemm(M, N, K, r, glu)) {
     allow_large_lds();
     hf::MidArgs a{};
     a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.sx = sx; a.sw = sw;
