@@ -325,6 +325,12 @@ constexpr double kPlanBw = 5.0e12;  // sustained HBM bytes per second of the cos
 // One 128-byte K stage of one 256 x 256 tile at the sustained (power-bound) matrix-core rate.
 constexpr double kTileStageSeconds = 2.0 * 256 * 256 * 128 / (8192.0 * 2.0e9 * 0.55);
 
+// The split-K finishing pass: a launch and a few microseconds of latency, then the int32 partial planes read and the
+// bf16 output written (measured: M=512, N=K=4096 in 4 splits, 29.4 us with the GEMM against 29.5 us estimated).
+double split_finish_seconds(int64_t splits, int64_t M, int64_t N) {
+  return 4e-6 + (4.0 * splits + 2.0) * (double)M * (double)N / kPlanBw;
+}
+
 GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
   GemmPlan best;
   const int64_t ntiles = (N + hf::kSkinnyN - 1) / hf::kSkinnyN;
@@ -353,6 +359,7 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
   const double fixed_bytes = (double)N * K + (double)M * K + 2.0 * M * N;
   best.seconds = std::max((double)((tiles + cus - 1) / cus) * stages * kTileStageSeconds, fixed_bytes / kPlanBw);
   if (tiles >= cus || stages < 4) return best;
+  const double t_whole = best.seconds;
   for (int64_t s = 2; s <= std::min<int64_t>(stages / 2, hf::kMaxSplits); ++s) {
     const int64_t chunk = (stages + s - 1) / s;
     const int64_t splits = (stages + chunk - 1) / chunk;
@@ -366,7 +373,20 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K) {
       best.k_chunk = (int)(chunk * hf::GBK);
     }
   }
+  // The split plan's partial planes are written during the GEMM and read back by the finishing pass after it: when
+  // that pass makes the split slower than one round of whole tiles, the tiles stay whole (M=2048, N=K=5120: 160
+  // whole tiles against 3 splits that took 92 us with their finishing pass).
+  if (best.splits > 1 && t_whole <= best.seconds + split_finish_seconds(best.splits, M, N)) {
+    best.splits = 1;
+    best.k_chunk = (int)(stages * hf::GBK);
+    best.seconds = t_whole;
+  }
   return best;
+}
+
+// The persistent GEMM's whole time as planned: the GEMM launch, plus the finishing pass of a split plan.
+double persistent_seconds(const GemmPlan& p, int64_t M, int64_t N) {
+  return p.seconds + (p.splits > 1 || p.skinny ? split_finish_seconds(p.splits, M, N) : 0.0);
 }
 
 // Whether a GEMM runs as 256 x 128 tiles (mid_gemm_kernel): its 256 x 256 tiles are fewer than the CUs, it is too
@@ -385,11 +405,19 @@ bool use_mid_gemm(int64_t M, int64_t N, int64_t K, int32_t r, bool glu) {
   const int64_t ntiles = (N + hf::kSkinnyN - 1) / hf::kSkinnyN;
   if (M <= 128 || (M <= hf::kSkinnyMaxM && 2 * ntiles <= cus)) return false;
   const int64_t tiles = tiles_m * ((N + hf::kMidBN - 1) / hf::kMidBN);
+  const double stages = (double)((K + hf::kMidBK - 1) / hf::kMidBK);
+  const double t_round = 0.9 * stages + 3.0;  // us per round of tiles
+  if (tiles > cus) {
+    // A second, partly filled round: only when it beats the persistent GEMM's plan (whole tiles, or split with its
+    // finishing pass). M=640-1024, N=15360, K=5120: 83-90 us in two rounds against 72-80 us persistent; M=1792,
+    // N=5120: 77 us in two rounds.
+    const double t_tiles = 1e-6 * t_round * (double)((tiles + cus - 1) / cus);
+    return t_tiles < persistent_seconds(gemm_plan(M, N, K), M, N);
+  }
   if (2 * tiles >= cus) return true;
   if (4 * tiles < cus) return false;
-  const double stages = (double)((K + hf::kMidBK - 1) / hf::kMidBK);
-  const double t_tiles = 0.9 * stages + 3.0, t_split = 21.0 + 0.62e-9 * 2.0 * (double)M * (double)N * (double)K;
-  return t_tiles < t_split;
+  const double t_split = 21.0 + 0.62e-9 * 2.0 * (double)M * (double)N * (double)K;
+  return t_round < t_split;
 }
 
 // Whether a GEMM of at most 64 rows runs in one pass (skinny_fused_kernel): its 32-row weight slices fill between a
