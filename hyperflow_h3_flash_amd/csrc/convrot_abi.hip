@@ -435,9 +435,11 @@ bool use_skinny_fused(int64_t M, int64_t N) {
 // half full, its tiles keep a few CUs busy for a whole tile time while the others idle. Peeling off the trailing
 // tile rows so the main part fills one round fewer, and splitting the peeled rows' K over every CU, turns that round
 // into a fraction of one, plus the partial planes, the finishing pass and a drain between the launches. A lightly
-// loaded last round runs at a higher clock than a full one (the full chip is power-bound), so it is priced at half
-// a round: peeling pays for deep K (M=37710, N=5376, K=14336: 2656 -> 2607 us) and not at K near 5000 (K=5376 and
-// 7168 within 1 %, M=41344, N=13824, K=5120 1 % slower), which this price leaves unpeeled. Returns M when nothing is
+// loaded last round runs at a higher clock than a full one (the full chip is power-bound): at K=5120 one tenth of a
+// round measured 0.61 of a full round's time (M=3584 against M=3072, N=5120), so the light round is priced at 0.6
+// of a round against the peeled rows' GEMM with its finishing pass (persistent_seconds). Measured with this price:
+// M=3584, N=K=5120 127.1 -> 114.8 us, M=7168 193.4 -> 180.3 us; deep K as before (M=37710, N=5376, K=14336:
+// 2656 -> 2607 us against no peel); the model's q/k/v and M=41344, N=13824 unchanged. Returns M when nothing is
 // peeled; the peeled GEMM's workspace is gemm_ws_bytes of the peeled rows.
 int64_t main_gemm_rows(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles_m = (M + hf::GBM - 1) / hf::GBM, tiles_n = (N + hf::GBN - 1) / hf::GBN;
@@ -451,8 +453,7 @@ int64_t main_gemm_rows(int64_t M, int64_t N, int64_t K) {
   const GemmPlan tail = gemm_plan(m_tail, N, K);
   if (tail.splits <= 1) return M;
   const double t_round = (double)((K + hf::GBK - 1) / hf::GBK) * kTileStageSeconds;
-  const double t_finish = 10e-6 + (8.0 * tail.splits + 2.0) * m_tail * N / kPlanBw;  // launch + partials + output
-  return tail.seconds + t_finish < 0.5 * t_round ? rows_main * hf::GBM : M;
+  return persistent_seconds(tail, m_tail, N) < 0.6 * t_round ? rows_main * hf::GBM : M;
 }
 
 // Ints per split-K partial plane: ceil(M / 32) x ceil(N / 32) blocks of 32 x 32 (partial_block_offset).
