@@ -3,10 +3,11 @@
 The library picks, by M, N and the device's CU count C: the single-pass few-row GEMM (M <= 64 and between C / 4 and C
 slices of 32 weight rows), the split few-row GEMM with its finishing pass, the 256 x 128 tiles of the mid-size GEMM,
 and the persistent 256 x 256 tiles (whole or split over K). The shapes below sit at those thresholds (computed from
-the device's C), with ragged N and M and K values that end inside a 128-byte stage. Bars: without a low-rank branch
-and bias, codes, scales and outputs bitwise the oracle's; with a rank-32 branch and a bias, every output within one
-bf16 ulp of the oracle's fused definition on the device's own low-rank intermediate (the bars of the other GEMM
-tests).
+the device's C), with ragged N and M and K values that end inside a 128-byte stage, and shapes on either side of
+the measured cost models' choices (whole tiles against a K split, a second round of mid-size tiles). Bars: without
+a low-rank branch and bias, codes, scales and outputs bitwise the oracle's; with a rank-32 branch and a bias, every
+output within one bf16 ulp of the oracle's fused definition on the device's own low-rank intermediate (the bars of
+the other GEMM tests).
 """
 
 from __future__ import annotations
@@ -44,6 +45,9 @@ def _shapes():
         (1000, 1040, 2064, 0),
         # persistent 256 x 256 tiles: one round exactly, one tile more, ragged edges
         (4096, 256, 4096, 0), (4100, 256, 4112, 32), (2048, 256, 8192, 0),
+        # fewer 256 x 256 tiles than CUs where whole tiles beat a K split, and where a second round of mid-size
+        # tiles loses to them
+        (2048, 1024, 5120, 0), (640, 1024, 15360, 32),
     ]
 
 
