@@ -97,3 +97,17 @@ def test_argument_checks_reject_before_launching(lib):
                                      1 << 15, 4, 1 << 16, 128, null, 0, null) == -5
     # sizes beyond the kernels' index range
     assert lib.hf_int8_gemm_i32(fake, 1 << 24, fake, 128, fake, 64, 4, 64, 128, null) == -5
+
+
+def test_split_planner_follows_the_measured_cost_models(lib):
+    """The workspace size query reports whether a GEMM splits K (or peels its trailing tile rows into a split GEMM):
+    0 means whole tiles. The choices below are the ones the measured cost models make on MI355X's 256 CUs (the
+    count the library assumes when no device answers, as here): whole tiles where one round of them beats the split
+    with its finishing pass (M=2048, N=K=5120: 65 against 85 us), a split where the tiles would leave three quarters
+    of the CUs idle (M=512, N=4096, K=5120), a peel of the rows that would leave the last round a tenth full
+    (M=3584, N=K=5120: 115 against 127 us), and whole tiles for the headline shape, whose 7680 tiles fill 30 rounds."""
+    assert lib.hf_int8_linear_ws_bytes(2048, 5120, 5120) == 0
+    assert lib.hf_int8_linear_ws_bytes(512, 4096, 5120) > 0
+    assert lib.hf_int8_linear_ws_bytes(3584, 5120, 5120) > 0
+    assert lib.hf_int8_linear_ws_bytes(32768, 15360, 5120) == 0
+    assert lib.hf_int8_linear_ws_bytes(37710, 5376, 14336) > 0  # the model's down projection: peeled
