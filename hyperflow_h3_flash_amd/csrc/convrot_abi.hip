@@ -391,7 +391,8 @@ double persistent_seconds(const GemmPlan& p, int64_t M, int64_t N) {
 
 // Whether a GEMM runs as 256 x 128 tiles (mid_gemm_kernel): its 256 x 256 tiles are fewer than the CUs, it is too
 // tall for the 128-row weight slices (skinny_gemm_kernel), and the 256 x 128 tiles fill at least half the CUs, so no
-// K split (with its int32 partial planes and finishing pass) is needed. Between a quarter and half of the CUs the
+// K split (with its int32 partial planes and finishing pass) is needed, unless K is deep enough for the split to
+// win clearly (below). Between a quarter and half of the CUs the
 // tiles' single round is weighed against the split path with times measured on MI355X (M=512-1024, N=2048-5120,
 // K=2048-5120, graph replays): the tiles take ~0.9 us per 128-byte K stage plus ~3 us, the split GEMM and its
 // finishing pass ~21 us plus ~0.62 us per 10^9 int8 operations (e.g. M=1024, N=K=3072: 25.5 against 31.8 us; at
@@ -414,7 +415,12 @@ bool use_mid_gemm(int64_t M, int64_t N, int64_t K, int32_t r, bool glu) {
     const double t_tiles = 1e-6 * t_round * (double)((tiles + cus - 1) / cus);
     return t_tiles < persistent_seconds(gemm_plan(M, N, K), M, N);
   }
-  if (2 * tiles >= cus) return true;
+  if (2 * tiles >= cus) {
+    // One round of tiles, at least half the CUs: they win unless K is deep enough that the persistent GEMM's split
+    // plan is clearly (10 %) faster. M=1024, N=5120, K=14336: 108.0 us as these tiles, 94.8 us split; at K=8192
+    // the estimates are within 2 % and the tiles are faster (61.3 against 63.2 us).
+    return persistent_seconds(gemm_plan(M, N, K), M, N) >= 0.9e-6 * t_round;
+  }
   if (4 * tiles < cus) return false;
   const double t_split = 21.0 + 0.62e-9 * 2.0 * (double)M * (double)N * (double)K;
   return t_round < t_split;
