@@ -239,8 +239,15 @@ bool lowrank_by_rows(int64_t M, int64_t K) {
   return M <= hf::kLrRowMaxRows && K <= (int64_t)hf::kLrRowMaxWaves * 1024;
 }
 
+// Whether the row kernel is also the faster choice. Its cost grows with M * K while the split MFMA kernel's stays
+// nearly flat over few rows: measured (M up to 384, rank 64) the rows win while M * K <= ~1.7 M (up to 384 rows at
+// K=3072, ~330 at K=5120, ~240 at K=7168, ~110 at K=14336) and lose beyond, by up to 2.2x (M=384, K=14336: 37.3
+// against 16.7 us).
+constexpr double kLrRowMaxWork = 1.7e6;
+bool lowrank_rows_faster(int64_t M, int64_t K) { return lowrank_by_rows(M, K) && (double)M * K <= kLrRowMaxWork; }
+
 int64_t lowrank_ws_bytes(int64_t M, int64_t K, int32_t r) {
-  if (lowrank_by_rows(M, K)) return 0;
+  if (lowrank_rows_faster(M, K)) return 0;
   const LrPlan p = lowrank_plan(M, K);
   return p.splits > 1 ? (int64_t)p.splits * M * r * 4 : 0;
 }
@@ -255,7 +262,14 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
     return HF_ERR_ALIGNMENT;
   if (M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (lowrank_by_rows(M, K)) {
+  bool by_rows = lowrank_rows_faster(M, K);
+  if (!by_rows && lowrank_by_rows(M, K)) {
+    // The split MFMA kernel wins here only with its workspace; without one the rows are still the faster choice.
+    const LrPlan p = lowrank_plan(M, K);
+    by_rows = p.splits > 1 && (!ws || !aligned(ws, 16) ||
+                               ws_bytes < (int64_t)p.splits * M * std::min<int32_t>(r, hf::kLrRanks) * 4);
+  }
+  if (by_rows) {
     const int64_t waves = (K + 1023) / 1024, groups = (r + hf::kLrRowRanks - 1) / hf::kLrRowRanks;
     const int64_t blocks = hf::lowrank_row_blocks(M, r);
     if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;

@@ -118,16 +118,22 @@ def test_split_lowrank_down_matches_oracle(oracle_lib, m, k, r):
                                    (33, 16384, 136), (200, 3072, 40), (250, 7168, 64), (9, 2048, 12), (5, 1024, 1),
                                    (384, 5120, 32)])
 def test_lowrank_down_by_rows_matches_oracle(oracle_lib, m, k, r):
-    """Up to 384 rows the down projection runs a workgroup per row and 8 ranks (no split, no workspace): within the
-    fp32-sum bound of the oracle's exactly rounded sum, bitwise on almost every element; a partial last 1024-element
-    tile (K=5376), the widest row (K=16384), rank counts of 1 to 17 groups of 8 and ranks that are not a multiple
-    of 8 (12, 1)."""
+    """Up to 384 rows, without a workspace, the down projection runs a workgroup per row and 8 ranks (no split):
+    within the fp32-sum bound of the oracle's exactly rounded sum, bitwise on almost every element; a partial last
+    1024-element tile (K=5376), the widest row (K=16384), rank counts of 1 to 17 groups of 8 and ranks that are not
+    a multiple of 8 (12, 1). With a workspace the same rows take the row kernel while M * K <= 1.7e6 (the size query
+    then asks for none) and the split MFMA kernel beyond (250 x 7168, 384 x 5120)."""
     from hyperflow_h3_flash_amd import _native
-    from hyperflow_h3_flash_amd.int8 import lowrank_down
 
-    assert _native.library().hf_lowrank_down_ws_bytes(m, k, r) == 0, "this shape should take the row path"
+    lib = _native.library()
+    assert (lib.hf_lowrank_down_ws_bytes(m, k, r) == 0) == (m * k <= 1.7e6)
     inp = oracle_lib.make_inputs(m, k, 8, 256, rank=r, seed=k + r + m)
-    u = lowrank_down(to_dev_bf16(inp["x"]), to_dev_bf16(inp["down"]))
+    x, down = to_dev_bf16(inp["x"]), to_dev_bf16(inp["down"])
+    u = torch.empty(m, r, device=DEV, dtype=torch.bfloat16)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.hf_lowrank_down(ctypes.c_void_p(x.data_ptr()), k, ctypes.c_void_p(down.data_ptr()), k,
+                               ctypes.c_void_p(u.data_ptr()), r, m, k, r, stream) == 0
+    torch.cuda.synchronize()
     got = oracle_lib.bf16_to_f32(bits_of(u))
     ref = oracle_lib.bf16_to_f32(oracle_lib.lowrank_down(inp["x"], inp["down"]))
     assert within_fp32_sum_bound(got, ref, oracle_lib.bf16_to_f32(inp["x"]), oracle_lib.bf16_to_f32(inp["down"]))
