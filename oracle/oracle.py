@@ -312,16 +312,27 @@ def swiglu(y_bits: np.ndarray, gate_first: bool = False) -> np.ndarray:
 
 def make_inputs(m: int, k: int, n: int, group: int, *, rank: int = 0, bias: bool = False,
                 outlier_frac: float = 0.01, outlier_scale: float = 20.0, seed: int = 0,
-                weight_dist: str = "uniform") -> dict:
+                weight_dist: str = "uniform", x_rows=None) -> dict:
     """Deterministic synthetic inputs of the benchmark's distributions (numpy PCG64, one seed, fixed draw order:
     x, outlier channels, qweight, wscale, down, up, bias).
 
     x ~ N(0, 1) with ceil(p*K) outlier channels scaled in float32 before the single bf16 cast. ``weight_dist``
     "uniform" draws qweight ~ U{-127..127} and wscale ~ U(1e-3, 1e-2); "quantized" draws W ~ 0.02 N(0,1) and
     quantizes it with `quantize_weight` (the reference tests' recipe, tests/test_int8.py:93-99).
+
+    ``x_rows`` (sorted row indices) keeps only those rows of x: the whole stream is still drawn, in blocks of rows
+    (the same values as one draw), so the other tensors are unchanged; for checks on a few rows of a large shape.
     """
     rng = np.random.default_rng(seed)
-    x = rng.standard_normal((m, k)).astype(np.float32)
+    if x_rows is None:
+        x = rng.standard_normal((m, k)).astype(np.float32)
+    else:
+        x_rows = np.asarray(x_rows, dtype=np.int64)
+        x = np.empty((x_rows.size, k), dtype=np.float32)
+        for r0 in range(0, m, 1024):
+            block = rng.standard_normal((min(1024, m - r0), k))
+            sel = (x_rows >= r0) & (x_rows < r0 + block.shape[0])
+            x[sel] = block[x_rows[sel] - r0]
     n_out = int(np.ceil(outlier_frac * k)) if outlier_frac > 0 else 0
     if n_out:
         cols = rng.choice(k, size=n_out, replace=False)

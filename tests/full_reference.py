@@ -13,7 +13,9 @@ import os
 import numpy as np
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "full")
-FULL_FIXTURES = ("full_cfg1", "full_cfg2")
+FULL_FIXTURES = ("full_cfg1", "full_cfg2", "full_cfg3_down", "full_cfg4_qkv")
+#: the fixtures whose outputs the oracle recomputes on the moved and sampled rows only (too large for every row)
+LARGE_FIXTURES = FULL_FIXTURES[1:]
 
 
 def load(name: str) -> dict:
@@ -21,12 +23,13 @@ def load(name: str) -> dict:
         return {key: z[key] for key in z.files}
 
 
-def inputs(fx: dict) -> dict:
+def inputs(fx: dict, x_rows=None) -> dict:
+    """The fixture's inputs, rebuilt from its seed; with `x_rows` (sorted) only those rows of x."""
     from oracle import oracle as O
 
     m, k, n, g = (int(v) for v in fx["shape"])
     return O.make_inputs(m, k, n, g, outlier_frac=float(fx["outlier_frac"]),
-                         outlier_scale=float(fx["outlier_scale"]), seed=int(fx["seed"]))
+                         outlier_scale=float(fx["outlier_scale"]), seed=int(fx["seed"]), x_rows=x_rows)
 
 
 def patched_digest(a: np.ndarray, idx: np.ndarray, ref_values: np.ndarray) -> str:

@@ -12,11 +12,12 @@ K=5120, N=15360, the headline workload) the outputs are too large to commit, so 
 
 So a device output equal to the oracle everywhere becomes the reference's output once the listed positions are set
 to the reference's values, which the digests confirm over every element (``tests/test_gpu_full_reference.py``).
+Also config 3's FFN down projection (M=32768, K=13824, N=5120) and config 4's token count (M=41344) at the QKV width.
 
 The reference path is ``Int8RotLinear.forward`` on CPU tensors (``_forward_torch``, int8.py:173-179), loaded from
 ``src/hyperflow_h3_flash/int8.py`` by file path as in ``make_golden.py``. The oracle's rows are computed for every
 row (rotation and quantization) and, for the output, on the rows whose codes or scale differ plus a sample.
-``python tests/golden/make_golden_full.py``.
+``python tests/golden/make_golden_full.py [name ...]``.
 """
 
 from __future__ import annotations
@@ -43,6 +44,9 @@ from make_golden import Recorder, bits, from_bits, load_reference  # noqa: E402
 FULL = [
     ("full_cfg1", (1024, 3072, 3072, 256), dict(outlier_frac=0.01, outlier_scale=20.0, seed=21)),
     ("full_cfg2", (32768, 5120, 15360, 256), dict(outlier_frac=0.005, outlier_scale=30.0, seed=22)),
+    # config 3's FFN down projection (deep K) and config 4's token count (40320 video + 1024 audio) at the QKV width
+    ("full_cfg3_down", (32768, 13824, 5120, 256), dict(outlier_frac=0.005, outlier_scale=30.0, seed=23)),
+    ("full_cfg4_qkv", (41344, 5120, 15360, 256), dict(outlier_frac=0.005, outlier_scale=30.0, seed=24)),
 ]
 SAMPLE_ROWS = 8
 
@@ -91,7 +95,10 @@ def main():
     ref = load_reference()
     meta = f"torch={torch.__version__} cpu={platform.processor() or platform.machine()} threads={torch.get_num_threads()}"
     rng = np.random.default_rng(2024)
+    only = set(sys.argv[1:])  # fixture names to (re)write; all of them when none is given
     for name, shape, opts in FULL:
+        if only and name not in only:
+            continue
         m, k, n, g = shape
         t0 = time.time()
         inputs = O.make_inputs(m, k, n, g, **opts)

@@ -1,7 +1,8 @@
 """The reference's own CPU path at two benchmark sizes against the oracle (CPU).
 
 The fixtures (tests/golden/full/*.npz) hold the reference ``Int8RotLinear.forward`` on CPU tensors at M=1024,
-K=N=3072 (config 1's layer) and M=32768, K=5120, N=15360 (the headline QKV projection), as digests plus every
+K=N=3072 (config 1's layer), M=32768, K=5120, N=15360 (the headline QKV projection), M=32768, K=13824, N=5120
+(config 3's FFN down projection) and M=41344, K=5120, N=15360 (config 4's token count), as digests plus every
 position where it differs from the exact-sum definition. These tests check what the fixtures claim about those
 differences, and that the oracle reproduces the reference everywhere else on the rows it can afford to recompute:
 
@@ -10,8 +11,8 @@ differences, and that the oracle reproduces the reference everywhere else on the
   code moves by one;
 * no scale differs, and every output that differs lies in a row whose codes differ;
 * config 1: the oracle's codes and scales of all 1024 rows give the reference's digest after the listed positions
-  are set; config 2: the oracle's codes and outputs of the moved rows match the listed values, and its outputs of
-  the sampled rows are the reference's.
+  are set; the larger ones: the oracle's codes and outputs of the moved rows match the listed values, and its outputs
+  of the sampled rows are the reference's.
 
 The device is checked against the same digests in test_gpu_full_reference.py.
 """
@@ -23,21 +24,23 @@ import hashlib
 import numpy as np
 import pytest
 
-from full_reference import FULL_FIXTURES, inputs, load, patched_digest
+from full_reference import FULL_FIXTURES, LARGE_FIXTURES, inputs, load, patched_digest
 from golden_utils import classify_rotation_mismatches
 
 
-def check_rotation_differences(fx: dict, x_bits: np.ndarray, oracle_lib) -> None:
-    """Every listed rotated-value difference is explained by the reference's fp32 accumulation."""
+def check_rotation_differences(fx: dict, x_bits: np.ndarray, x_row_ids: np.ndarray, oracle_lib) -> None:
+    """Every listed rotated-value difference is explained by the reference's fp32 accumulation. `x_bits` holds the
+    rows `x_row_ids` (sorted) of x, among them every row with a listed difference."""
     k, g = int(fx["shape"][1]), int(fx["shape"][3])
     rows = np.unique(fx["xr_idx"] // k)
-    exact = oracle_lib.rotate(x_bits[rows], g)
+    x_rows = x_bits[np.searchsorted(x_row_ids, rows)]
+    exact = oracle_lib.rotate(x_rows, g)
     other = exact.copy()
     pos = {int(r): i for i, r in enumerate(rows)}
     for flat, ref_v, orc_v in zip(fx["xr_idx"], fx["xr_ref"], fx["xr_oracle"]):
         assert exact[pos[int(flat // k)], int(flat % k)] == orc_v
         other[pos[int(flat // k)], int(flat % k)] = ref_v
-    count, unexplained = classify_rotation_mismatches(x_bits[rows], exact, other, g, limit=10**6)
+    count, unexplained = classify_rotation_mismatches(x_rows, exact, other, g, limit=10**6)
     assert count == fx["xr_idx"].size and not unexplained, unexplained[:5]
 
 
@@ -63,7 +66,7 @@ def test_config1_codes_and_scales_all_rows(oracle_lib):
     g = int(fx["shape"][3])
     xr = oracle_lib.rotate(inp["x"], g)
     sx, xq = oracle_lib.quantize(xr)
-    check_rotation_differences(fx, inp["x"], oracle_lib)
+    check_rotation_differences(fx, inp["x"], np.arange(inp["x"].shape[0]), oracle_lib)
     assert np.array_equal(sx.view(np.uint32), fx["sx"].view(np.uint32))
     assert patched_digest(xq, fx["xq_idx"], fx["xq_ref"]) == str(fx["xq_sha256"])
     rows = fx["sample_rows"]
@@ -71,14 +74,16 @@ def test_config1_codes_and_scales_all_rows(oracle_lib):
     assert np.array_equal(y, fx["y_sample"])
 
 
-def test_config2_moved_and_sampled_rows(oracle_lib):
-    fx = load("full_cfg2")
+@pytest.mark.parametrize("name", LARGE_FIXTURES)
+def test_moved_and_sampled_rows(oracle_lib, name):
+    fx = load(name)
     m, k, n, g = (int(v) for v in fx["shape"])
-    inp = inputs(fx)
     moved = np.unique(fx["xq_idx"] // k)
     rows = np.union1d(moved, fx["sample_rows"])
-    check_rotation_differences(fx, inp["x"], oracle_lib)
-    xr = oracle_lib.rotate(inp["x"][rows], g)
+    need = np.union1d(rows, np.unique(fx["xr_idx"] // k))  # only these rows of x are kept
+    inp = inputs(fx, x_rows=need)
+    check_rotation_differences(fx, inp["x"], need, oracle_lib)
+    xr = oracle_lib.rotate(inp["x"][np.searchsorted(need, rows)], g)
     sx, xq = oracle_lib.quantize(xr)
     assert np.array_equal(sx.view(np.uint32), fx["sx"][rows].view(np.uint32))
     # The listed code differences are exactly where the oracle's codes of the moved rows differ from the listed
