@@ -1,4 +1,4 @@
-"""The reference's own CPU path at two benchmark sizes against the oracle (CPU).
+"""The reference's own CPU path at four benchmark sizes against the oracle (CPU).
 
 The fixtures (tests/golden/full/*.npz) hold the reference ``Int8RotLinear.forward`` on CPU tensors at M=1024,
 K=N=3072 (config 1's layer), M=32768, K=5120, N=15360 (the headline QKV projection), M=32768, K=13824, N=5120
