@@ -42,12 +42,10 @@ constexpr int kSlotBytes = kAStage + kBStage;     // 64 KiB
 constexpr int kRingBytes = 2 * kSlotBytes;        // 128 KiB
 constexpr int kParamBytes = 3 * 256 * 4;          // the tile's sx, wscale and bias (fp32)
 constexpr int kGemmLds = kRingBytes + kParamBytes;
-#ifndef HF_GEMM_WAVES
-#define HF_GEMM_WAVES 8
-#endif
-// Waves per workgroup: 8 = 2 (m) x 4 (n) waves of 128 x 64 (two per SIMD), 4 = 2 x 2 waves of 128 x 128 (one per
-// SIMD, accumulators in AGPRs, a third fewer LDS fragment reads per MFMA).
-constexpr int kWaves = HF_GEMM_WAVES;
+// Waves per workgroup: 2 (m) x 4 (n) waves of 128 x 64, two per SIMD. The index arithmetic below is written for
+// any even count, but only 8 is built: 4 waves of 128 x 128 (one per SIMD, accumulators in AGPRs) measured slower,
+// and the pair-order (SwiGLU) epilogue is laid out for 8.
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int WN = 2 * GBN / kWaves;              // n columns per wave
 constexpr int NB = WN / 32;                       // 32-column MFMA blocks per wave
