@@ -60,6 +60,9 @@ def parse_args():
     p.add_argument("--rows", type=int, default=None, help="--config 5: only this M (64, 256 or 1024)")
     p.add_argument("--copy-probe", action="store_true",
                    help="only copy a 1 GiB device buffer 3 times (calibrates the HBM byte counters) and exit")
+    p.add_argument("--ceilings", action="store_true",
+                   help="only measure the device's ceilings (INT8 MFMA with no memory traffic, a device copy's "
+                        "bandwidth) and exit; the headline run reports them too")
     p.add_argument("--vendor-gemm", action="store_true",
                    help="only time the vendor library's own INT8, FP8 and bf16 GEMMs at the headline shape (a "
                         "calibration of what the matrix cores sustain, not this build's path) and exit")
@@ -98,6 +101,51 @@ def copy_probe(torch):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_probe_bytes_per_launch": src.numel() * 4}), flush=True)
+
+
+def ceilings(torch, repeats=5):
+    """Measured ceilings of this device, beside the published peaks: the INT8 matrix cores' rate with no memory
+    traffic (libhf_ceilings.so, one 8-wave workgroup per CU issuing independent v_mfma_i32_32x32x32_i8) on zero
+    operands and on uniform random codes, whose bit toggling sets the clock the chip holds, and the bandwidth of a
+    1 GiB device-to-device copy (read + write bytes). Each figure is the mean of `repeats` launches after two."""
+    from hyperflow_h3_flash_amd import _native
+
+    lib = _native.ceilings_library()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    rounds, grid = 12000, cus
+    out = torch.empty(grid * 512, dtype=torch.int32, device=dev)
+
+    def mean_seconds(launch):
+        for _ in range(2):
+            launch()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        e[0].record(stream)
+        for _ in range(repeats):
+            launch()
+        e[1].record(stream)
+        torch.cuda.synchronize()
+        return e[0].elapsed_time(e[1]) * 1e-3 / repeats
+
+    result = {}
+    tables = {"zero": torch.zeros(8192, dtype=torch.int8, device=dev),
+              "uniform": torch.randint(-127, 128, (8192,), dtype=torch.int8, device=dev, generator=gen)}
+    ops = 2.0 * lib.hf_ceiling_mfma_i8_macs(rounds, grid)
+    for name, table in tables.items():
+        def launch():
+            rc = lib.hf_ceiling_mfma_i8(table.data_ptr(), rounds, grid, out.data_ptr(), stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"hf_ceiling_mfma_i8 failed: {rc}")
+        t = mean_seconds(launch)
+        result[f"mfma_int8_{name}_TOPS"] = round(ops / t / 1e12, 1)
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    t = mean_seconds(lambda: dst.copy_(src))
+    result["copy_GBs"] = round(2.0 * src.numel() * 4 / t / 1e9, 1)
+    del src, dst
+    return result
 
 
 def make_inputs(torch, dev, seed=0):
@@ -239,6 +287,10 @@ def main():
     if args.copy_probe:
         copy_probe(torch)
         return
+    if args.ceilings:
+        print(json.dumps({"ceilings": ceilings(torch), "published": {"mfma_int8_TOPS": PEAK_INT8_TOPS,
+                                                                      "hbm_GBs": PEAK_HBM_GBS}}), flush=True)
+        return
     if args.config != 2:
         for line in run_config(torch, args.config, args.steps, args.warmup, rows=args.rows,
                                cpu_rows=0 if args.no_cpu_baseline else args.cpu_rows):
@@ -329,6 +381,12 @@ def main():
         },
         "cpu_baseline": None,
     }
+    # The GEMM's rate against what the matrix cores hold on random codes with no memory traffic, and the rotation
+    # pass against a device copy's bandwidth (measured after the timed region).
+    ceil = ceilings(torch)
+    ceil["gemm_frac_of_mfma_uniform"] = round(gemm_tops / ceil["mfma_int8_uniform_TOPS"], 4)
+    ceil["rotate_quant_frac_of_copy"] = round(result["rotate_quant_GBs"] / ceil["copy_GBs"], 4)
+    result["ceilings"] = ceil
     if not args.no_cpu_baseline:
         del x, layer
         torch.cuda.empty_cache()

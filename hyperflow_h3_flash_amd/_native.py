@@ -15,6 +15,9 @@ PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PACKAGE_DIR)
 LIB_PATH = os.path.join(PACKAGE_DIR, "libhf_convrot.so")
 SOURCE = os.path.join(PACKAGE_DIR, "csrc", "convrot_abi.hip")
+#: The benchmark's calibration kernels (matrix-core ceiling), a library of their own outside the C ABI.
+CEILINGS_LIB_PATH = os.path.join(PACKAGE_DIR, "libhf_ceilings.so")
+CEILINGS_SOURCE = os.path.join(PACKAGE_DIR, "csrc", "ceilings.hip")
 ARCH = "gfx950"
 
 #: hipcc flags: CDNA4 only; fp-contract off keeps every multiply and add separately rounded as written; packed
@@ -75,17 +78,23 @@ def hipcc() -> str:
     return path if os.path.exists(path) else "hipcc"
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compile csrc/ into libhf_convrot.so for gfx950 (always recompiles). Returns the library path."""
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, SOURCE]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
+def _compile(source: str, target: str, verbose: bool) -> None:
+    tmp = target + ".tmp"
+    proc = subprocess.run([hipcc(), *HIPCC_FLAGS, "-o", tmp, source], capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
+        raise RuntimeError(f"hipcc failed ({proc.returncode}) on {source}:\n{proc.stderr[-4000:]}")
     if verbose and proc.stderr:
         print(proc.stderr[-2000:])
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, target)
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile csrc/ into libhf_convrot.so, and the benchmark's libhf_ceilings.so, for gfx950 (always recompiles).
+    Returns the convrot library's path."""
+    _compile(SOURCE, LIB_PATH, verbose)
+    _compile(CEILINGS_SOURCE, CEILINGS_LIB_PATH, verbose)
     library.cache_clear()
+    ceilings_library.cache_clear()
     return LIB_PATH
 
 
@@ -105,6 +114,20 @@ def library() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = argtypes
         fn.restype = restype
+    return lib
+
+
+@lru_cache(maxsize=None)
+def ceilings_library() -> ctypes.CDLL:
+    """The benchmark's calibration library (csrc/ceilings.hip). Raises RuntimeError when it is missing."""
+    if not os.path.exists(CEILINGS_LIB_PATH):
+        raise RuntimeError(f"{CEILINGS_LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+                           "g.build()'`")
+    lib = ctypes.CDLL(CEILINGS_LIB_PATH)
+    lib.hf_ceiling_mfma_i8.argtypes = [_P, _I32, _I32, _P, _P]
+    lib.hf_ceiling_mfma_i8.restype = ctypes.c_int
+    lib.hf_ceiling_mfma_i8_macs.argtypes = [_I32, _I32]
+    lib.hf_ceiling_mfma_i8_macs.restype = ctypes.c_int64
     return lib
 
 

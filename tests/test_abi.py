@@ -111,3 +111,16 @@ def test_split_planner_follows_the_measured_cost_models(lib):
     assert lib.hf_int8_linear_ws_bytes(3584, 5120, 5120) > 0
     assert lib.hf_int8_linear_ws_bytes(32768, 15360, 5120) == 0
     assert lib.hf_int8_linear_ws_bytes(37710, 5376, 14336) > 0  # the model's down projection: peeled
+
+
+def test_ceilings_library_loads_and_rejects_bad_arguments():
+    """The benchmark's calibration library (matrix-core ceiling) is built beside the C ABI's and checks its
+    arguments before launching anything."""
+    if not os.path.exists(_native.CEILINGS_LIB_PATH):
+        pytest.fail(f"{_native.CEILINGS_LIB_PATH} not built: run __graft_entry__.build()")
+    lib = _native.ceilings_library()
+    assert lib.hf_ceiling_mfma_i8_macs(12000, 256) == 256 * 8 * 12000 * 8 * 32**3
+    buf = ctypes.create_string_buffer(16)
+    assert lib.hf_ceiling_mfma_i8(None, 1, 1, buf, None) == -1
+    assert lib.hf_ceiling_mfma_i8(buf, 0, 1, buf, None) == -1
+    assert lib.hf_ceiling_mfma_i8(buf, 1, 0, buf, None) == -1
