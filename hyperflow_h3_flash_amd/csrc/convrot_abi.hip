@@ -133,12 +133,17 @@ int launch_rotate_wide(bool f32_recip, int lg, const uint16_t* x, int64_t ldx, i
   return launch_status();
 }
 
-// rotate_quant_reg_kernel<lg, tpw> (both already range-checked by the caller).
-int launch_rotate_reg(int lg, int tpw, dim3 grid, dim3 block, size_t lds, hipStream_t s, const uint16_t* x,
-                      int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int K, int wpr) {
+// rotate_quant_reg_kernel<lg, tpw, f32> (lg and tpw already range-checked by the caller).
+int launch_rotate_reg(int lg, int tpw, bool f32, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                      const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int K, int wpr) {
 #define HF_RQ_CASE(L, T)                                                                                          \
   if (lg == L && tpw == T) {                                                                                      \
-    hipLaunchKernelGGL((hf::rotate_quant_reg_kernel<L, T>), grid, block, lds, s, x, ldx, q, ldq, sx, M, K, wpr);   \
+    if (f32)                                                                                                      \
+      hipLaunchKernelGGL((hf::rotate_quant_reg_kernel<L, T, true>), grid, block, lds, s, x, ldx, q, ldq, sx, M, K, \
+                         wpr);                                                                                    \
+    else                                                                                                          \
+      hipLaunchKernelGGL((hf::rotate_quant_reg_kernel<L, T, false>), grid, block, lds, s, x, ldx, q, ldq, sx, M,   \
+                         K, wpr);                                                                                 \
     return launch_status();                                                                                       \
   }
 #define HF_RQ_CASES(L) HF_RQ_CASE(L, 1) HF_RQ_CASE(L, 2) HF_RQ_CASE(L, 3) HF_RQ_CASE(L, 4) HF_RQ_CASE(L, 5)
@@ -150,6 +155,22 @@ int launch_rotate_reg(int lg, int tpw, dim3 grid, dim3 block, size_t lds, hipStr
 #undef HF_RQ_CASES
 #undef HF_RQ_CASE
   return HF_ERR_ARGUMENT;
+}
+
+// Rows of at most 4 * kRqRegMaxTpw tiles held in registers (rotate_quant_reg_kernel): wpr waves of tpw tiles per
+// row, 4 / wpr rows per workgroup. The caller has checked the group, the alignment and M > 0.
+int rotate_rows_in_registers(bool f32, int lg, const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx,
+                             int64_t M, int64_t K, hipStream_t s) {
+  const int64_t ntiles = (K + hf::kRqTile - 1) / hf::kRqTile;
+  const int wpr = (int)((ntiles + hf::kRqRegMaxTpw - 1) / hf::kRqRegMaxTpw);
+  const int tpw = (int)((ntiles + wpr - 1) / wpr);
+  const int rows_per_wg = std::max(1, 4 / wpr);
+  const int nw = wpr * rows_per_wg;
+  const int64_t blocks = (M + rows_per_wg - 1) / rows_per_wg;
+  if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+  allow_large_lds();
+  return launch_rotate_reg(lg, tpw, f32, dim3((unsigned)blocks), dim3(64 * nw), hf::rotate_quant_reg_lds_bytes(nw),
+                           s, x, ldx, q, ldq, sx, M, (int)K, wpr);
 }
 
 int check_gemm_operands(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, int64_t M, int64_t N,
@@ -654,17 +675,7 @@ int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, floa
     }
     return launch_status();
   }
-  if (ntiles <= 4 * hf::kRqRegMaxTpw) {
-    // Rows held in registers: wpr waves of tpw tiles per row, 4 / wpr rows per workgroup.
-    const int wpr = (int)((ntiles + hf::kRqRegMaxTpw - 1) / hf::kRqRegMaxTpw);
-    const int tpw = (int)((ntiles + wpr - 1) / wpr);
-    const int rows_per_wg = std::max(1, 4 / wpr);
-    const int nw = wpr * rows_per_wg;
-    const int64_t blocks = (M + rows_per_wg - 1) / rows_per_wg;
-    if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;
-    return launch_rotate_reg(lg, tpw, dim3((unsigned)blocks), dim3(64 * nw), hf::rotate_quant_reg_lds_bytes(nw), s,
-                             x, ldx, q, ldq, sx, M, (int)K, wpr);
-  }
+  if (ntiles <= 4 * hf::kRqRegMaxTpw) return rotate_rows_in_registers(false, lg, x, ldx, q, ldq, sx, M, K, s);
   const size_t lds = hf::rotate_quant_lds_bytes(waves, (int)K);
   const int64_t blocks64 = (M + waves - 1) / waves;
   const unsigned blocks = (unsigned)std::min<int64_t>(blocks64, int64_t(1) << 30);
@@ -691,6 +702,9 @@ int hf_rotate_quant_ex(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, f
   if (K >= (int64_t(1) << 30)) return HF_ERR_SIZE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (lg >= 6) return launch_rotate_wide(true, lg, x, ldx, q, ldq, sx, M, K, s);
+  // Up to 20 tiles the row stays in registers and x is read once; wider rows take the two-pass kernel below.
+  if ((K + hf::kRqTile - 1) / hf::kRqTile <= 4 * hf::kRqRegMaxTpw)
+    return rotate_rows_in_registers(true, lg, x, ldx, q, ldq, sx, M, K, s);
   constexpr int waves = 4;
   const size_t lds = hf::rotate_quant_f32_recip_lds_bytes(waves);
   const unsigned blocks = (unsigned)std::min<int64_t>((M + waves - 1) / waves, int64_t(1) << 30);

@@ -152,9 +152,9 @@ __device__ __forceinline__ float rotate_tile_packed(uint4 cur0, uint4 cur1, int 
   return amax;
 }
 
-// rotate_tile_f64, then every value rounded once to bf16, returned as fp32 values (the layout of held_offset), with
-// this lane's absmax of the rounded, still unnormalised sums.
-template <int LOG4G>
+// rotate_tile_f64, then every value rounded once to bf16 (F32: to fp32), returned as fp32 values (the layout of
+// held_offset), with this lane's absmax of the rounded, still unnormalised sums.
+template <int LOG4G, bool F32 = false>
 __device__ __forceinline__ float rotate_tile_rounded(uint4 cur0, uint4 cur1, int lane, double* scratch,
                                                      float (&f)[16]) {
   float amax = 0.0f;
@@ -162,7 +162,7 @@ __device__ __forceinline__ float rotate_tile_rounded(uint4 cur0, uint4 cur1, int
   rotate_tile_f64<LOG4G>(cur0, cur1, lane, scratch, v);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    f[i] = round_f64_to_bf16_value(v[i]);
+    f[i] = F32 ? (float)v[i] : round_f64_to_bf16_value(v[i]);
     amax = fmaxf(amax, fabsf(f[i]));
   }
   return amax;
@@ -417,7 +417,10 @@ size_t rotate_quant_reg_lds_bytes(int waves) { return (size_t)waves * kRqScratch
 
 // Five tiles per wave held as fp32 (80 VGPRs; 118 in all with the wave index and the row descriptor in scalar
 // registers) leave four waves per SIMD (three with the 1024 group's second transpose).
-template <int LOG4G, int TPW>
+//
+// F32: the arithmetic of the reference's GPU kernels (rotate_quant_f32_recip_kernel's: each sum rounded once to
+// fp32, codes by the reciprocal multiply) in this one-pass layout; the rounded row is held in the same registers.
+template <int LOG4G, int TPW, bool F32>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TPW == kRqRegMaxTpw ? (LOG4G == 5 ? 3 : 4) : 1)))
 void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
                              float* __restrict__ s, int64_t M, int K, int wpr) {
@@ -458,7 +461,7 @@ void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t
                                __float_as_uint(held[i][3]));
     const uint4 b = make_uint4(__float_as_uint(held[i][4]), __float_as_uint(held[i][5]), __float_as_uint(held[i][6]),
                                __float_as_uint(held[i][7]));
-    amax = fmaxf(amax, rotate_tile_rounded<LOG4G>(a, b, lane, scratch, held[i]));
+    amax = fmaxf(amax, rotate_tile_rounded<LOG4G, F32>(a, b, lane, scratch, held[i]));
   }
   amax = wave_max(amax);
   float m = amax;
@@ -471,14 +474,31 @@ void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t
     for (int w = 0; w < wpr; ++w) m = fmaxf(m, maxes[(wave / wpr) * wpr + w]);
   }
   if (!live) return;
-  const RowScale rs = row_scale<LOG4G>(m);
-  if (part == 0 && lane == 0) s[row] = rs.sx;
   int8_t* qrow = q + row * ldq;
   unsigned char* stage = reinterpret_cast<unsigned char*>(scratch);  // the transpose area is free from here on
+  if constexpr (F32) {
+    // rotate_quant_f32_recip_kernel's scale and codes (|xr * inv| <= 127: the clamp never acts on finite input).
+    const float sx = fmaxf(ldexpf(m, -LOG4G), 1e-12f) / 127.0f;
+    const float inv_n = ldexpf(1.0f / sx, -LOG4G);
+    if (part == 0 && lane == 0) s[row] = sx;
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const int base = (t0 + i) * kRqTile;
-    if (base < K) quantize_store_tile<LOG4G>(held[i], rs, base, K, lane, stage, qrow);
+    for (int i = 0; i < TPW; ++i) {
+      const int base = (t0 + i) * kRqTile;
+      if (base < K) {
+        uint32_t codes[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) codes[j] = __float_as_uint(held[i][j] * inv_n + kRoundMagic);
+        store_codes<LOG4G>(codes, base, K, lane, stage, qrow);
+      }
+    }
+  } else {
+    const RowScale rs = row_scale<LOG4G>(m);
+    if (part == 0 && lane == 0) s[row] = rs.sx;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int base = (t0 + i) * kRqTile;
+      if (base < K) quantize_store_tile<LOG4G>(held[i], rs, base, K, lane, stage, qrow);
+    }
   }
 }
 
@@ -628,8 +648,10 @@ template __global__ void rotate_quant_wide_kernel<false>(const uint16_t*, int64_
 template __global__ void rotate_quant_wide_kernel<true>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int, int);
 
 #define HF_RQ_REG(L, T)                                                                                            \
-  template __global__ void rotate_quant_reg_kernel<L, T>(const uint16_t*, int64_t, int8_t*, int64_t, float*,       \
-                                                         int64_t, int, int);
+  template __global__ void rotate_quant_reg_kernel<L, T, false>(const uint16_t*, int64_t, int8_t*, int64_t, float*,\
+                                                                int64_t, int, int);                               \
+  template __global__ void rotate_quant_reg_kernel<L, T, true>(const uint16_t*, int64_t, int8_t*, int64_t, float*, \
+                                                               int64_t, int, int);
 #define HF_RQ_REG_ALL(L) HF_RQ_REG(L, 1) HF_RQ_REG(L, 2) HF_RQ_REG(L, 3) HF_RQ_REG(L, 4) HF_RQ_REG(L, 5)
 HF_RQ_REG_ALL(1)
 HF_RQ_REG_ALL(2)

@@ -35,12 +35,17 @@ def bits_of(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("group", [4, 16, 64, 256])
+# Rows of up to 20 tiles of 1024 are held in registers (1 to 4 waves per row, ragged last waves); wider rows take the
+# two-pass kernel. Group 1024 adds a radix-4 stage after a second transpose.
+@pytest.mark.parametrize("group", [4, 16, 64, 256, 1024])
 @pytest.mark.parametrize("m,k", [(1, 256), (7, 1280), (65, 2304), (130, 5120), (1029, 5376), (33, 14336),
-                                 (2, 98304)])
+                                 (9, 20480), (3, 21504), (2, 98304)])
 def test_f32_recip_matches_the_oracle(oracle_lib, group, m, k):
     from hyperflow_h3_flash_amd.int8 import rotate_quant
 
+    if k % group:
+        pytest.skip(f"K={k} is not a multiple of the group {group}")
+    print(f"f32_recip rotation M={m} K={k} G={group}", flush=True)
     inp = oracle_lib.make_inputs(m, k, 8, group, outlier_frac=0.01, outlier_scale=30.0, seed=m + k + group)
     q, s = rotate_quant(to_dev_bf16(inp["x"]), group, arithmetic="f32_recip")
     sx, xq = oracle_lib.quantize_recip(oracle_lib.rotate_f32(inp["x"], group))
