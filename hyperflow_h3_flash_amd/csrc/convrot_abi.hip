@@ -98,6 +98,10 @@ void allow_large_lds() {
     HF_LR_ATTR(1, 4) HF_LR_ATTR(1, 5) HF_LR_ATTR(1, 6) HF_LR_ATTR(1, 7) HF_LR_ATTR(1, 8)
     HF_LR_ATTR(2, 4) HF_LR_ATTR(2, 5) HF_LR_ATTR(2, 6) HF_LR_ATTR(2, 7) HF_LR_ATTR(2, 8)
 #undef HF_LR_ATTR
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_wide_kernel<4>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::lw_lds(4));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_wide_kernel<5>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::lw_lds(5));
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_up_kernel),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kUpLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::rotate_quant_wide_kernel<false>),
@@ -306,6 +310,26 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
                           !aligned(ws, 16))) {
     plan = LrPlan{};  // no (or too small a) workspace: one pass over K
     plan.k_chunk = (int)K;
+  }
+  if (plan.splits == 1 && r > hf::kLrRanks) {
+    // Ranks past 64 with many rows: 256 ranks per pass over x (lowrank_down_wide_kernel), 4 or 5 row blocks of 32
+    // per workgroup (5 when 128-row workgroups would need more than one round of CUs).
+    if (2 * hf::kLwRanks * ld_down >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+    const int nr = (M + 127) / 128 > device_cus() ? 5 : 4;
+    const unsigned blocks = (unsigned)((M + 32 * nr - 1) / (32 * nr));
+    for (int32_t j0 = 0; j0 < r; j0 += hf::kLwRanks) {
+      const int rr = std::min<int32_t>(hf::kLwRanks, r - j0);
+      const uint16_t* d = down + (int64_t)j0 * ld_down;
+      if (nr == 5)
+        hipLaunchKernelGGL(hf::lowrank_down_wide_kernel<5>, dim3(blocks), dim3(128 * 5), hf::lw_lds(5), s, x, ldx, d,
+                           ld_down, u + j0, ldu, (int)M, (int)K, rr);
+      else
+        hipLaunchKernelGGL(hf::lowrank_down_wide_kernel<4>, dim3(blocks), dim3(128 * 4), hf::lw_lds(4), s, x, ldx, d,
+                           ld_down, u + j0, ldu, (int)M, (int)K, rr);
+      const int st = launch_status();
+      if (st != HF_OK) return st;
+    }
+    return HF_OK;
   }
   float* part = plan.splits > 1 ? static_cast<float*>(ws) : nullptr;
   // Waves per workgroup (32 rows each): the fewest that cover the rows in one round of one workgroup per CU, from 4

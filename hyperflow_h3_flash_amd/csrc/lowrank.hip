@@ -169,6 +169,103 @@ HF_LR_DOWN(1, 4) HF_LR_DOWN(1, 5) HF_LR_DOWN(1, 6) HF_LR_DOWN(1, 7) HF_LR_DOWN(1
 HF_LR_DOWN(2, 4) HF_LR_DOWN(2, 5) HF_LR_DOWN(2, 6) HF_LR_DOWN(2, 7) HF_LR_DOWN(2, 8)
 #undef HF_LR_DOWN
 
+// Ranks past 64 (the standalone low-rank linear's ranks are typically several hundred): lowrank_down_kernel would
+// stream x once per 64 ranks. This kernel takes 256 ranks per pass over x: a workgroup of NR row blocks of 32 rows
+// has two waves per row block, each multiplying its 32 rows against 128 of the ranks (four 32 x 32 MFMA blocks, the
+// fragment layout and summation order of lowrank_down_kernel, so every u element is the same sum). A stage is the
+// 32 NR x 64 slab of x and the 256 x 64 slab of down (48 or 52 KiB), in a 3-stage ring. Every wave issues the same
+// six loads per stage (two of the x blocks of 8 rows, four of the 32 down blocks; with NR = 5 the last two waves
+// load the first down blocks again: the same bytes to the same place).
+constexpr int kLwRanks = 256;  // ranks per pass
+constexpr int kLwStages = 3;
+__host__ __device__ constexpr int lw_stage_bytes(int nr) { return nr * 32 * kLrStageK * 2 + kLwRanks * kLrStageK * 2; }
+__host__ __device__ constexpr int lw_lds(int nr) { return kLwStages * lw_stage_bytes(nr); }
+
+template <int NR>
+__global__ __launch_bounds__(128 * NR, 1) void lowrank_down_wide_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                       const uint16_t* __restrict__ down,
+                                                                       int64_t ldd, uint16_t* __restrict__ u,
+                                                                       int64_t ldu, int M, int K, int r) {
+  constexpr int kRows = 32 * NR;
+  constexpr int kXBytes = kRows * kLrStageK * 2;
+  constexpr int kStageBytes = lw_stage_bytes(NR);
+  constexpr int kRB = 4;  // 32-rank blocks per wave
+  static_assert(lw_lds(NR) <= 160 * 1024, "ring exceeds the LDS");
+  static_assert((kRows / 8) % (2 * NR) == 0 && (kRows / 8) / (2 * NR) == 2, "two x blocks per wave");
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lw_smem_raw[];
+  unsigned char HF_LDS* smem = (unsigned char HF_LDS*)lw_smem_raw;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane & 31, half = lane >> 5;
+  const int rblock = wave % NR, rhalf = wave / NR;  // this wave's 32 rows and 128 ranks
+  const int m0 = blockIdx.x * kRows;
+  const int rows_m = min(kRows, M - m0);
+  const uint32_t ldx_bytes = (uint32_t)ldx * 2u, ldd_bytes = (uint32_t)ldd * 2u;
+  const uint32_t bytes_x = (uint32_t)rows_m * ldx_bytes, bytes_d = (uint32_t)r * ldd_bytes;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (int64_t)m0 * ldx, bytes_x);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(down, bytes_d);
+
+  // Stages past the end load zeros, so "stage t has landed" is always vmcnt(6): one later stage (6 loads) in flight.
+  auto issue = [&](int t) {
+    unsigned char HF_LDS* st = smem + (t % kLwStages) * kStageBytes;
+    lr_load<2, kCpolStream>(rx, bytes_x, ldx_bytes, rows_m, t * kLrStageK, K, st, wave * 2, lane);
+    lr_load<4>(rd, bytes_d, ldd_bytes, r, t * kLrStageK, K, st + kXBytes, (wave * 4) % 32, lane);
+  };
+
+  v16f acc[kRB];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) acc[rb] = (v16f){0};
+  const bool live = rhalf * 128 < r;  // a wave whose ranks are all past r only loads
+  const int nst = (K + kLrStageK - 1) / kLrStageK;
+#pragma unroll
+  for (int t = 0; t < kLwStages - 1; ++t) issue(t);
+  const int xrow = rblock * 32 + sub;
+  for (int t = 0; t < nst; ++t) {
+    // This wave's loads of stage t have landed and its reads of slot (t - 1) % 3 have returned; the barrier makes
+    // that true for every wave, so slot (t - 1) % 3 can take stage t + 2.
+    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(t + kLwStages - 1);
+    if (!live) continue;
+    const unsigned char HF_LDS* st = smem + (t % kLwStages) * kStageBytes;
+#pragma unroll
+    for (int s = 0; s < kLrStageK / 16; ++s) {
+      const int c = 2 * s + half;
+      const v8bf xf = *reinterpret_cast<const v8bf HF_LDS*>(st + xrow * 128 + lr_swizzle(xrow, c) * 16);
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb) {
+        const int drow = rhalf * 128 + rb * 32 + sub;
+        const v8bf df =
+            *reinterpret_cast<const v8bf HF_LDS*>(st + kXBytes + drow * 128 + lr_swizzle(drow, c) * 16);
+        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(df, xf, acc[rb], 0, 0, 0);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // zero-fill loads past the end may still be landing
+
+  const int row = m0 + xrow;
+  if (row >= M || !live) return;
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int j = rhalf * 128 + rb * 32 + 8 * g + 4 * half;
+      uint16_t* dst = u + (int64_t)row * ldu + j;
+      if (j + 3 < r && (ldu & 3) == 0) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(acc[rb][4 * g], acc[rb][4 * g + 1]),
+                                                    pack_bf16x2(acc[rb][4 * g + 2], acc[rb][4 * g + 3]));
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (j + e < r) dst[e] = (uint16_t)f32_to_bf16_rne(acc[rb][4 * g + e]);
+      }
+    }
+  }
+}
+
+template __global__ void lowrank_down_wide_kernel<4>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
+                                                     int64_t, int, int, int);
+template __global__ void lowrank_down_wide_kernel<5>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
+                                                     int64_t, int, int, int);
+
 constexpr int kMaxSplits = 32;  // K chunks of a split launch, at most
 
 // u[m, j] = bf16(sum_s part[s][m][j]): the planes added in a fixed order, one rounding (round to nearest even).

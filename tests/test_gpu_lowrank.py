@@ -150,3 +150,37 @@ def test_device_layer_without_the_library_raises(monkeypatch):
     lr = LowRankLinear(256, 64, 8).to(device=DEV, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="HIP library"):
         lr(torch.randn(4, 256, device=DEV, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("m,k,r", [(16500, 1040, 72), (20000, 5376, 256), (17000, 2048, 200), (33000, 1024, 320),
+                                   (33000, 1024, 512), (37710, 5376, 128)])
+def test_wide_rank_down_projection(oracle_lib, m, k, r):
+    """Ranks past 64 with more rows than half the CUs' 128-row workgroups cover (no K split) take 256 ranks per pass
+    over x (lowrank_down_wide_kernel): the same sums, in the same order, as 64-rank passes of the unsplit rank-64
+    kernel (bitwise). Against the exact sums s (float64, sampled rows): bitwise the oracle's exactly rounded value on
+    almost every element, and everywhere within the fp32 accumulation bound, |u - s| <= 2^-8 |s| + (1 + 2^-8) K
+    2^-24 sum_k |x_k d_k| (a sum that cancels to near zero can miss one bf16 ulp of itself). M=33000 and 37710 use
+    workgroups of five row blocks, and r=320 and 512 two passes."""
+    from hyperflow_h3_flash_amd import _native
+    from hyperflow_h3_flash_amd.int8 import _stream, lowrank_down
+
+    print(f"wide-rank low-rank down M={m} K={k} r={r}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(m + k + r)
+    x = (torch.randn(m, k, device=DEV, generator=gen) * 2.0).to(torch.bfloat16)
+    down = (torch.randn(r, k, device=DEV, generator=gen) * 0.05).to(torch.bfloat16)
+    u = lowrank_down(x, down)
+    lib = _native.library()
+    ref = torch.empty(m, r, device=DEV, dtype=torch.bfloat16)
+    for j0 in range(0, r, 64):
+        rr = min(64, r - j0)
+        assert lib.hf_lowrank_down(x.data_ptr(), k, down[j0:].data_ptr(), k, ref[:, j0:].data_ptr(), r, m, k, rr,
+                                   _stream(DEV)) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(u, ref)
+    rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(r).choice(m, 24, replace=False)]))
+    xs, ds = bits_of(x[rows]), bits_of(down)
+    got = oracle_lib.bf16_to_f32(bits_of(u[rows])).astype(np.float64)
+    xf, df = oracle_lib.bf16_to_f32(xs).astype(np.float64), oracle_lib.bf16_to_f32(ds).astype(np.float64)
+    exact_sum, mag = xf @ df.T, np.abs(xf) @ np.abs(df).T
+    assert (np.abs(got - exact_sum) <= 2.0**-8 * np.abs(exact_sum) + (1 + 2.0**-8) * k * 2.0**-24 * mag).all()
+    assert (bits_of(u[rows]) == oracle_lib.lowrank_down(xs, ds)).mean() > 0.98
