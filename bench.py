@@ -24,6 +24,8 @@ parity-test shapes and supporting measurements, not the headline line):
      the up-projection's GEMM epilogue)
   7  the model's own linear shapes (K, N) on the 5.2 s clip's M=37710 tokens, rank 64: q/k/v 5376->7168 each,
      the fused q/k/v 5376->21504, out 7168->5376, gated up 5376->28672, down 14336->5376
+  8  the standalone low-rank linear up(down(x)) (the model's non-INT8 linears) at M=37710, K->N 5376->7168 and
+     14336->5376, ranks 64, 256 and 512: TFLOP/s of 2 M r (K + N), with the vendor library's bf16 GEMMs beside it
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--config N [--rows M]]
 """
@@ -55,7 +57,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=32768, help="row sample for the CPU baseline")
-    p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6, 7),
+    p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6, 7, 8),
                    help="workload: 2 (default) is the headline QKV projection; 1, 3-7 are supporting measurements")
     p.add_argument("--rows", type=int, default=None, help="--config 5: only this M (64, 256 or 1024)")
     p.add_argument("--copy-probe", action="store_true",
@@ -524,6 +526,34 @@ def run_config(torch, config, steps, warmup, rows=None, cpu_rows=2048):
                        config={"workload": f"model linear ({name})", "M": m, "K": k, "N": n, "group": GROUP,
                                "rank": 64, "bias": False})
             del x, layer
+            torch.cuda.empty_cache()
+    elif config == 8:
+        # The standalone low-rank linear (the model's non-INT8 linears, transformer.py:48-72): y = up(down(x)) in
+        # bf16 with a bf16 intermediate. Work 2 M r (K + N); the vendor library's bf16 GEMMs (torch's own
+        # up(down(x))) are timed on the same tensors beside it.
+        from hyperflow_h3_flash_amd import LowRankLinear
+
+        m = 37710
+        gen = torch.Generator(device=dev).manual_seed(8)
+        for k, n in ((5376, 7168), (14336, 5376)):
+            x = torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16)
+            for r in (64, 256, 512):
+                layer = LowRankLinear(k, n, r).to(dev).to(torch.bfloat16)
+                with torch.no_grad():
+                    layer.down.weight.copy_(torch.randn(r, k, device=dev, generator=gen) * 0.02)
+                    layer.up.weight.copy_(torch.randn(n, r, device=dev, generator=gen) * 0.02)
+                    t = timed(torch, lambda: layer(x), steps, warmup)
+                    t_vendor = timed(torch, lambda: layer.up(layer.down(x)), steps, warmup)
+                flops = 2.0 * m * r * (k + n)
+                nbytes = 2 * m * k + 2 * r * (k + n) + 4 * m * r + 2 * m * n
+                yield dict(base, dtype="bf16", metric=f"low-rank linear TFLOP/s, M={m} K={k} N={n} rank {r}",
+                           unit="TFLOP/s", value=round(flops / t / 1e12, 1), ms_per_step=round(t * 1e3, 4),
+                           higher_is_better=True, hbm_GBs=round(nbytes / t / 1e9, 1),
+                           vendor_ms=round(t_vendor * 1e3, 4),
+                           config={"workload": "standalone low-rank linear up(down(x))", "M": m, "K": k, "N": n,
+                                   "rank": r})
+                del layer
+            del x
             torch.cuda.empty_cache()
     else:
         k = 5120
