@@ -52,7 +52,7 @@ SIGNATURES = {
     "hf_lowrank_down": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I32, _P], ctypes.c_int),
     "hf_lowrank_down_ws_bytes": ([_I64, _I64, _I32], ctypes.c_int64),
     "hf_lowrank_down_ws": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I32, _P, _I64, _P], ctypes.c_int),
-    "hf_int8_linear_ws_bytes": ([_I64, _I64, _I64], ctypes.c_int64),
+    "hf_int8_linear_ws_bytes": ([_I64, _I64, _I64, _I32, _I32], ctypes.c_int64),
     "hf_int8_linear_ws": ([_P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P, _I64, _I64, _I64, _I64, _P,
                            _I64, _P], ctypes.c_int),
     "hf_int8_linear_act_ws": ([_P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _I64, _I64, _I64,
@@ -61,7 +61,7 @@ SIGNATURES = {
     "hf_int8_linear": ([_P, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
                        ctypes.c_int),
     "hf_int8_gemm_i32": ([_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P], ctypes.c_int),
-    "hf_convrot_linear_ws_bytes": ([_I64, _I64, _I64, _I32], ctypes.c_int64),
+    "hf_convrot_linear_ws_bytes": ([_I64, _I64, _I64, _I32, _I32], ctypes.c_int64),
     "hf_convrot_linear_ws": ([_P, _I64, _P, _P, _I32, _I32, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _P, _I32, _I32,
                               _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P], ctypes.c_int),
     "hf_convrot_linear": ([_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _P, _I32, _P, _P, _P, _P, _I64, _I64,

@@ -20,8 +20,9 @@ own names (``transformer_blocks.<i>.attn.to_q`` ... ``ff.net.2``):
 
 Not fixed by the reference tree (it lives in ComfyUI and comfy-kitchen, absent here): what ``int8_tensorwise``'s
 scale multiplies and whether the released INT8 weights carry the block-Hadamard rotation of the convrot format. The
-reader moves the tensors as they are into ``Int8RotLinear`` (which rotates its input with the module's ``group``);
-a checkpoint whose weights were not quantized in the rotated basis would need its own conversion.
+reader moves the tensors as they are into ``Int8RotLinear`` (which rotates its input with the module's ``group``)
+only when the file's metadata names that group (``convrot_group``) or the caller vouches for the basis
+(``rotated=True``); a checkpoint whose weights were not quantized in the rotated basis needs its own conversion.
 """
 
 from __future__ import annotations
@@ -74,11 +75,12 @@ def check_metadata(path: str) -> dict[str, Any]:
     """The file's ``hyperflow`` metadata; RuntimeError when it is missing or its ``format`` is newer than 1."""
     info = hyperflow_metadata(path)
     if info is None:
-        raise RuntimeError(f"{path} is not a HyperFlow checkpoint (no `{METADATA_KEY}` metadata)")
+        raise RuntimeError(f"cannot read {path}: its safetensors header has no {METADATA_KEY!r} entry, so it is not "
+                           "a HyperFlow INT8 file")
     version = int(info.get("format", 0))
     if version > SUPPORTED_FORMAT:
-        raise RuntimeError(f"{path} uses HyperFlow layout {version}; this reader handles layouts up to "
-                           f"{SUPPORTED_FORMAT}")
+        raise RuntimeError(f"cannot read {path}: written in format {version}, and formats above {SUPPORTED_FORMAT} "
+                           "are unknown to this loader")
     return info
 
 
@@ -117,18 +119,32 @@ def _module(model: nn.Module, name: str) -> nn.Module:
     return owner[int(attr)] if isinstance(owner, nn.ModuleList) else getattr(owner, attr)
 
 
+#: Key of the ``hyperflow`` metadata entry that names the Hadamard group the INT8 weights were quantized in.
+GROUP_KEY = "convrot_group"
+
+
 @torch.no_grad()
-def load_comfy_checkpoint(model: nn.Module, path: str, group: int, *, prefix: str = "transformer_blocks"
-                          ) -> dict[str, list[str]]:
+def load_comfy_checkpoint(model: nn.Module, path: str, group: int, *, prefix: str = "transformer_blocks",
+                          rotated: bool = False) -> dict[str, list[str]]:
     """Load the block linears of a ComfyUI-layout HyperFlow file into ``model`` (reference module names).
 
     Dense ``nn.Linear`` targets are replaced by `Int8RotLinear(in, out, group)` for INT8 parts and by
     `LowRankLinear(in, out, rank)` for factorized parts; existing modules of those types are filled in place. Returns
     ``{"int8": [...], "lowrank": [...], "skipped": [...]}``: the model names filled, and the file's tensors that are
-    not block linears (left to the caller)."""
+    not block linears (left to the caller).
+
+    ``Int8RotLinear`` rotates its input by the block Hadamard of ``group``, so its weights must have been quantized
+    in that rotated basis. Nothing in the reference tree says whether the ComfyUI release's INT8 weights were: the
+    loader accepts INT8 parts only when the file's metadata names the group (``"convrot_group"``, which must equal
+    ``group``) or the caller states it with ``rotated=True``; otherwise it raises ValueError instead of loading
+    weights whose outputs would be silently wrong. Low-rank parts need neither."""
     from safetensors.torch import load_file
 
-    check_metadata(path)
+    info = check_metadata(path)
+    declared = info.get(GROUP_KEY)
+    if declared is not None and int(declared) != group:
+        raise ValueError(f"{path}: INT8 weights quantized for Hadamard group {declared}, loader asked for {group}")
+    basis_known = rotated or declared is not None
     parts, others = group_parts(load_file(path, device="cpu"))
     done: dict[str, list[str]] = {"int8": [], "lowrank": [], "skipped": sorted(others)}
     for (block, part), leaves in sorted(parts.items()):
@@ -147,6 +163,9 @@ def load_comfy_checkpoint(model: nn.Module, path: str, group: int, *, prefix: st
             target.up.weight.copy_(up.to(target.up.weight.dtype))
             done["lowrank"].append(name)
             continue
+        if not basis_known:
+            raise ValueError(f"{name}: the file does not say that its INT8 weights are in the block-Hadamard basis of "
+                             f"group {group} (no {GROUP_KEY!r} metadata); pass rotated=True if they are")
         weight, scale = leaves["weight"], leaves["weight_scale"]
         if weight.dtype != torch.int8:
             raise ValueError(f"{name}: INT8 weight stored as {weight.dtype}")
@@ -175,5 +194,5 @@ def load_comfy_checkpoint(model: nn.Module, path: str, group: int, *, prefix: st
     return done
 
 
-__all__ = ["INT8_FORMAT", "METADATA_KEY", "MODULE_NAMES", "PART", "SUPPORTED_FORMAT", "check_metadata",
+__all__ = ["GROUP_KEY", "INT8_FORMAT", "METADATA_KEY", "MODULE_NAMES", "PART", "SUPPORTED_FORMAT", "check_metadata",
            "decode_comfy_quant", "group_parts", "hyperflow_metadata", "load_comfy_checkpoint"]

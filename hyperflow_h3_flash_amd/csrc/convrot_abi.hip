@@ -505,7 +505,7 @@ bool use_skinny_fused(int64_t M, int64_t N) {
 // of a round against the peeled rows' GEMM with its finishing pass (persistent_seconds). Measured with this price:
 // M=3584, N=K=5120 127.1 -> 114.8 us, M=7168 193.4 -> 180.3 us; deep K as before (M=37710, N=5376, K=14336:
 // 2656 -> 2607 us against no peel); the model's q/k/v and M=41344, N=13824 unchanged. Returns M when nothing is
-// peeled; the peeled GEMM's workspace is gemm_ws_bytes of the peeled rows.
+// peeled; the peeled rows' workspace is that of their own route (gemm_route).
 int64_t main_gemm_rows(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles_m = (M + hf::GBM - 1) / hf::GBM, tiles_n = (N + hf::GBN - 1) / hf::GBN;
   const int64_t tiles = tiles_m * tiles_n, cus = device_cus();
@@ -524,11 +524,46 @@ int64_t main_gemm_rows(int64_t M, int64_t N, int64_t K) {
 // Ints per split-K partial plane: ceil(M / 32) x ceil(N / 32) blocks of 32 x 32 (partial_block_offset).
 int64_t partial_plane_ints(int64_t M, int64_t N) { return ((M + 31) / 32) * ((N + 31) / 32) * 1024; }
 
-int64_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K) {
+// The kernel path of a GEMM of these sizes, and the workspace that path uses. int8_linear_impl launches by it and the
+// size queries report its bytes, so a query gives exactly what the call with the same sizes, rank and activation
+// uses (0 for the 256 x 128 tiles, the one-pass few-row kernel and whole tiles).
+struct GemmRoute {
+  enum Kind { kWhole, kPeel, kMid, kSkinnyFused, kSplit } kind = kWhole;
+  int64_t m_main = 0;    // kPeel: rows run as whole tiles; the rest run by their own route
+  GemmPlan plan;         // kSplit: the K split
+  int64_t ws_bytes = 0;  // workspace the route uses (kPeel: the peeled rows' route's)
+};
+
+GemmRoute gemm_route(int64_t M, int64_t N, int64_t K, int32_t r, bool glu) {
+  GemmRoute route;
   const int64_t m_main = main_gemm_rows(M, N, K);
-  if (m_main < M) return gemm_ws_bytes(M - m_main, N, K);
-  const GemmPlan p = gemm_plan(M, N, K);
-  return (p.splits > 1 || p.skinny) ? (int64_t)p.splits * partial_plane_ints(M, N) * 4 : 0;
+  if (m_main < M) {
+    route.kind = GemmRoute::kPeel;
+    route.m_main = m_main;
+    route.ws_bytes = gemm_route(M - m_main, N, K, r, glu).ws_bytes;
+    return route;
+  }
+  if (use_mid_gemm(M, N, K, r, glu)) {
+    route.kind = GemmRoute::kMid;
+    return route;
+  }
+  if (use_skinny_fused(M, N)) {
+    route.kind = GemmRoute::kSkinnyFused;
+    return route;
+  }
+  route.plan = gemm_plan(M, N, K);
+  if (route.plan.splits > 1 || route.plan.skinny) {
+    route.kind = GemmRoute::kSplit;
+    route.ws_bytes = (int64_t)route.plan.splits * partial_plane_ints(M, N) * 4;
+  }
+  return route;
+}
+
+bool is_glu(int act_code) { return act_code == HF_ACT_SWIGLU || act_code == HF_ACT_SWIGLU_GATE_FIRST; }
+
+int64_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r, int act_code) {
+  if (M <= 0 || N <= 0 || K <= 0 || r < 0) return 0;
+  return gemm_route(M, N, K, r, is_glu(act_code)).ws_bytes;
 }
 
 int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
@@ -536,7 +571,7 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
                      const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
                      int64_t ws_bytes, hf_stream_t stream, int act_code = HF_ACT_NONE) {
   if (act_code < HF_ACT_NONE || act_code > HF_ACT_SWIGLU_GATE_FIRST) return HF_ERR_ARGUMENT;
-  const bool glu = act_code == HF_ACT_SWIGLU || act_code == HF_ACT_SWIGLU_GATE_FIRST;
+  const bool glu = is_glu(act_code);
   const int act = glu ? hf::kActSwiGLU : (act_code == HF_ACT_GELU_TANH ? hf::kActGeluTanh : hf::kActNone);
   // SwiGLU: the N weight rows are F hidden and F gate rows (F = N / 2 output columns), F a multiple of 16.
   if (glu && (N < 0 || N % 32)) return HF_ERR_ARGUMENT;
@@ -555,17 +590,21 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
   if (glu && (N * ldw >= (int64_t(1) << 32) || (r > 0 && N * ld_up * 2 >= (int64_t(1) << 32)))) return HF_ERR_SIZE;
   const int glu_half = (int)(N / 2), glu_gate_first = act_code == HF_ACT_SWIGLU_GATE_FIRST;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t m_main = main_gemm_rows(M, N, K);
-  if (m_main < M && ws && aligned(ws, 16) && ws_bytes >= gemm_ws_bytes(M - m_main, N, K)) {
-    // The trailing rows as a split-K GEMM (bitwise the same outputs: the partial sums are exact and the finishing
-    // pass applies the same epilogue), then the rest as whole tiles; the same stream orders the two.
+  const GemmRoute route = gemm_route(M, N, K, r, glu);
+  // A route that needs a workspace falls back to whole tiles when the caller's is missing or too small.
+  const bool ws_ok = route.ws_bytes == 0 || (ws && aligned(ws, 16) && ws_bytes >= route.ws_bytes);
+  if (route.kind == GemmRoute::kPeel && ws_ok) {
+    // The trailing rows by their own route (a split-K GEMM, or one of the few-row kernels; bitwise the same
+    // outputs: the partial sums are exact and every path applies the same epilogue), then the rest as whole tiles;
+    // the same stream orders the two.
+    const int64_t m_main = route.m_main;
     st = int8_linear_impl(q + m_main * ldq, ldq, w, ldw, sx + m_main, sw, r > 0 ? u + m_main * ldu : u, ldu, up,
                           ld_up, r, bias, y + m_main * ldy, ldy, M - m_main, N, K, ws, ws_bytes, stream, act_code);
     if (st != HF_OK) return st;
     return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, m_main, N, K, nullptr, 0,
                             stream, act_code);
   }
-  if (use_mid_gemm(M, N, K, r, glu)) {
+  if (route.kind == GemmRoute::kMid) {
     allow_large_lds();
     hf::MidArgs a{};
     a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.sx = sx; a.sw = sw;
@@ -581,7 +620,7 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
       hipLaunchKernelGGL(hf::mid_gemm_kernel<hf::kActNone>, grid, block, hf::kMidLds, s, a);
     return launch_status();
   }
-  if (use_skinny_fused(M, N)) {
+  if (route.kind == GemmRoute::kSkinnyFused) {
     // At most 64 rows: one pass, 32 weight rows per workgroup with the whole K, the epilogue in the same kernel.
     allow_large_lds();
     const int vec = aligned(y, 8) && (ldy % 4) == 0;
@@ -595,9 +634,9 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
 #undef HF_SF_LAUNCH
     return launch_status();
   }
-  const GemmPlan plan = gemm_plan(M, N, K);
+  const GemmPlan& plan = route.plan;
   const int64_t plane = partial_plane_ints(M, N);
-  if ((plan.splits > 1 || plan.skinny) && ws && aligned(ws, 16) && ws_bytes >= (int64_t)plan.splits * plane * 4) {
+  if (route.kind == GemmRoute::kSplit && ws_ok) {
     // Split K: int32 partial planes (block by block; in pair order with SwiGLU), then one pass that adds them and
     // applies the epilogue.
     if (plan.skinny) {
@@ -772,9 +811,8 @@ int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, c
   return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, M, N, K, nullptr, 0, stream);
 }
 
-int64_t hf_int8_linear_ws_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return gemm_ws_bytes(M, N, K);
+int64_t hf_int8_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r, int32_t activation) {
+  return gemm_ws_bytes(M, N, K, r, activation);
 }
 
 int hf_int8_linear_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
@@ -880,10 +918,10 @@ int rotate_lowrank_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, 
 
 extern "C" {
 
-int64_t hf_convrot_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
+int64_t hf_convrot_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r, int32_t activation) {
+  if (M <= 0 || N <= 0 || K <= 0 || r < 0) return 0;
   const int64_t lr = r > 0 ? lowrank_ws_bytes(M, K, std::min<int32_t>(r, hf::kLrRanks)) : 0;
-  return std::max<int64_t>(lr, gemm_ws_bytes(M, N, K));
+  return std::max<int64_t>(lr, gemm_ws_bytes(M, N, K, r, activation));
 }
 
 int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, int32_t quantized, int32_t arithmetic,
@@ -959,7 +997,7 @@ int hf_convrot_linear_noalloc(const uint16_t* x, int64_t ldx, int8_t* q, float* 
                               int64_t N, int64_t K, hf_stream_t stream) {
   if (M < 0 || N < 0 || K <= 0 || r < 0) return HF_ERR_ARGUMENT;
   if (M == 0 || N == 0) return HF_OK;
-  const int64_t need = hf_convrot_linear_ws_bytes(M, N, K, r);
+  const int64_t need = hf_convrot_linear_ws_bytes(M, N, K, r, activation);
   if (need > kScratchBytes) return HF_ERR_SCRATCH;
   void* ws = need > 0 ? scratch_address() : nullptr;
   if (need > 0 && !ws) return HF_ERR_LAUNCH;

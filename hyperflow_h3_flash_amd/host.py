@@ -2,7 +2,9 @@
 
 The reference runs its torch statements (`Int8RotLinear._forward_torch`, src/hyperflow_h3_flash/int8.py:173-179)
 for CPU tensors; a drop-in has to compute on the host too. This module evaluates the same definition as the gfx950
-kernels, so a layer gives the same bits on either side of the PCIe link:
+kernels. Without a low-rank term (with or without the bias) a layer gives the same bits on either side of the PCIe
+link; with one, the host sums the term exactly while the device's matrix cores sum it in fp32, so the two agree
+within one bf16 ulp (bitwise on almost every element):
 
 1. the rotated activation is the exact block sum ``x[m, gG:(g+1)G] @ H_G`` rounded once to bf16 (ties to even);
 2. ``sx = max(absmax_row, 1e-12) / 127`` and ``xq = clamp(round_half_even(xr / sx), -127, 127)`` in fp32, true
@@ -10,8 +12,10 @@ kernels, so a layer gives the same bits on either side of the PCIe link:
 3. ``acc = xq @ qweight^T`` as an exact integer;
 4. ``y = bf16((f32(acc) * sx) * wscale)``, two rounded fp32 products and one rounding to bf16;
 
-and the fused extension ``y = bf16((f32(acc) * sx) * wscale + bf16(x @ down^T) @ up^T + bias)`` with the low-rank
-product summed in float64 and one rounding, followed by the optional output activation of torch's own modules.
+and the fused extension ``y = bf16((f32(acc) * sx) * wscale + bf16(x @ down^T) @ up^T + bias)``: the bias alone
+added in fp32, a low-rank product (and the bias beside it) summed in float64; one rounding; then the optional output
+activation of torch's own modules. The low-rank intermediate ``bf16(x @ down^T)`` is the exact sum rounded once
+(the device's fp32 sum is within one bf16 ulp of it).
 
 Exactness: the rotation's products ``x * (+-2^-n)`` are exact and float64 holds their sums exactly while a group's
 nonzero inputs span fewer than about 37 binades (the device's fp64 butterfly: 33); the integer product is exact in
@@ -90,10 +94,14 @@ def lowrank_down(x2: Tensor, down: Tensor) -> Tensor:
 
 def dequantize(acc: Tensor, sx: Tensor, wscale: Tensor, *, u: Tensor | None = None, up: Tensor | None = None,
                bias: Tensor | None = None) -> Tensor:
-    """``bf16((f32(acc) * sx) * wscale [+ u @ up^T] [+ bias])``: the two fp32 products, then (extension) the
-    low-rank term and the bias added in float64 to the fp32 value, one rounding to bf16."""
+    """``bf16((f32(acc) * sx) * wscale [+ u @ up^T] [+ bias])``: the two fp32 products, then (extension) with the
+    bias alone one fp32 addition, as the device kernels make it; with a low-rank term the term and the bias added in
+    float64 to the fp32 value (the exact sum; the device sums in fp32 in an unspecified order). One rounding to
+    bf16."""
     y = (acc.to(torch.float32) * sx[:, None]) * wscale.to(torch.float32)[None, :]
-    if u is None and bias is None:
+    if u is None:
+        if bias is not None:
+            y = y + bias.to(torch.bfloat16).to(torch.float32)[None, :]
         return y.to(torch.bfloat16)
     s = y.to(torch.float64)
     if u is not None:

@@ -230,10 +230,10 @@ class Int8RotLinear(nn.Module):
             ws_ = ws_.to(torch.float32).contiguous()
         y = torch.empty(M, N // 2 if act in _GLU_CODES else N, device=dev, dtype=torch.bfloat16)
         lib = _native.library()
-        key = (M, N, K, r)
+        key = (M, N, K, r, act)
         nbytes = _ONE_CALL_WS.get(key)
         if nbytes is None:
-            nbytes = _ONE_CALL_WS[key] = lib.hf_convrot_linear_ws_bytes(M, N, K, r)
+            nbytes = _ONE_CALL_WS[key] = lib.hf_convrot_linear_ws_bytes(M, N, K, r, act)
         with torch.cuda.device(dev):
             work = torch.empty(nbytes, device=dev, dtype=torch.uint8) if nbytes > 0 else None
             status = lib.hf_convrot_linear_ws(
@@ -245,9 +245,10 @@ class Int8RotLinear(nn.Module):
         return y
 
     def _forward_torch(self, x2: Tensor, rot: Tensor | None = None) -> Tensor:
-        """The layer on host tensors (int8.py:173-179): ``host.py``'s evaluation of the device kernels' definition,
-        so the bits match the device's. ``rot`` is accepted for the reference's signature; the rotation is always
-        the regular Hadamard of ``self.group``."""
+        """The layer on host tensors (int8.py:173-179): ``host.py``'s evaluation of the device kernels' definition:
+        the device's bits without a low-rank term (with or without the bias), within one bf16 ulp of them with one
+        (the host sums the term exactly, the device in fp32). ``rot`` is accepted for the reference's signature; the
+        rotation is always the regular Hadamard of ``self.group``."""
         xq, sx = host.rotate_quant(x2, self.group)
         acc = host.int8_gemm_exact(xq, self.qweight)
         u = host.lowrank_down(x2, self.down.weight) if self.rank else None
@@ -423,7 +424,7 @@ def int8_matmul(a: Tensor, b: Tensor, sa: Tensor, sb: Tensor, *, u: Tensor | Non
     c = torch.empty(M, N // 2 if act in _GLU_CODES else N, device=a.device, dtype=torch.bfloat16)
     lib = _native.library()
     with torch.cuda.device(a.device):
-        ws, nbytes = _workspace(a.device, lib.hf_int8_linear_ws_bytes(M, N, K))
+        ws, nbytes = _workspace(a.device, lib.hf_int8_linear_ws_bytes(M, N, K, r, act))
         status = lib.hf_int8_linear_act_ws(
             _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(sa), _ptr(sb),
             _ptr(u), u.stride(0) if u is not None else 0, _ptr(up), up.stride(0) if up is not None else 0, r,

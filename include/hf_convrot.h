@@ -127,10 +127,11 @@ int hf_int8_linear(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, c
  * 256 x 256 tiles than the device has CUs (few rows), K is split across workgroups; their int32 partial accumulators (`ws`) are added
  * exactly and the same epilogue is applied, so the result equals hf_int8_linear's bit for bit. With many tiles
  * whose last round on the CUs would be less than half full and deep K, the trailing tile rows run that way and the
- * rest as whole tiles. `hf_int8_linear_ws_bytes` gives the bytes used for these sizes (0: no split); a NULL or
+ * rest as whole tiles. `hf_int8_linear_ws_bytes` gives the bytes the call with these sizes, rank and activation
+ * uses (0 when its kernels need none: whole tiles, the 256 x 128 tiles, the one-pass few-row kernel); a NULL or
  * smaller workspace runs the unsplit kernel. Replaces the same reference interface as hf_int8_linear (int8.py:376-390).
  */
-int64_t hf_int8_linear_ws_bytes(int64_t M, int64_t N, int64_t K);
+int64_t hf_int8_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r, int32_t activation);
 int hf_int8_linear_ws(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, const float* sx, const float* sw,
                       const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld_up, int32_t r,
                       const uint16_t* bias, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws,
@@ -184,10 +185,10 @@ int hf_convrot_linear(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t l
  *   quantized != 0: q and sx already hold x's codes and scales (the input shared by q/k/v projections,
  *                   int8.py:150-159), and x is read only by the low-rank term;
  * then, when r > 0, hf_lowrank_down_ws(x -> u [M, r] (ldu = r)), then hf_int8_linear_act_ws(q, ..., activation ->
- * y). `ws` serves both split-K passes (one after the other): hf_convrot_linear_ws_bytes gives its size (a NULL or
- * smaller workspace runs the unsplit kernels). Same rules as the calls it makes.
+ * y). `ws` serves both split-K passes (one after the other): hf_convrot_linear_ws_bytes gives its size for these
+ * sizes, rank and activation (a NULL or smaller workspace runs the unsplit kernels). Same rules as the calls it makes.
  */
-int64_t hf_convrot_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r);
+int64_t hf_convrot_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r, int32_t activation);
 int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, int32_t quantized, int32_t arithmetic,
                          const int8_t* w, int64_t ldw, const float* sw, const uint16_t* down, int64_t ld_down,
                          const uint16_t* up, int64_t ld_up, int32_t r, const uint16_t* bias, int32_t activation,
@@ -199,7 +200,8 @@ int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, i
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. It allocates
  * nothing: the split-K partial planes and low-rank partial sums live in a 64 MiB scratch array inside the library's
  * code object (hf_convrot_linear_noalloc_max_bytes), one per device, held until the process ends. A call that would
- * need more than that (hf_convrot_linear_ws_bytes(M, N, K, r) > 64 MiB) returns HF_ERR_SCRATCH and launches nothing.
+ * need more than that (hf_convrot_linear_ws_bytes(M, N, K, r, activation) > 64 MiB) returns HF_ERR_SCRATCH and launches
+ * nothing.
  * Calls on one device share its scratch: calls that overlap on one device (other streams, other host threads) race
  * and must be ordered by the caller. Otherwise exactly hf_convrot_linear_ws with a workspace of the needed size.
  */

@@ -406,8 +406,12 @@ void oracle_lowrank_down(const uint16_t* x, const uint16_t* down, int64_t M, int
     }
 }
 
-/* Fused extension: y = bf16( (f32(acc)*sx)*ws + sum_j u[m,j]*up[n,j] + bias[n] ), the low-rank sum in float64 and
- * one final rounding. up is [N, r] (LowRankLinear.up.weight); bias may be NULL, u/up NULL when r == 0. */
+/* Fused extension: y = bf16( (f32(acc)*sx)*ws + sum_j u[m,j]*up[n,j] + bias[n] ) with one final rounding to bf16.
+ * The sum is an fp32 sum (the extension's definition; the composition Int8RotLinear(x) + LowRankLinear(x) + bias of
+ * transformer.py:57-58 rounds to bf16 after every term instead). With a low-rank term (r > 0) the order of the fp32
+ * additions is unspecified, so the oracle takes the exact sum (float64) and device results are held to one bf16 ulp
+ * of it; with the bias alone the sum is the single fp32 addition fl32(v + bias), then one rounding to bf16.
+ * up is [N, r] (LowRankLinear.up.weight); bias may be NULL, u/up NULL when r == 0. */
 void oracle_fused_epilogue(const int32_t* acc, const float* sx, const float* ws, const uint16_t* u,
                            const uint16_t* up, int64_t r, const uint16_t* bias, int64_t M, int64_t N, uint16_t* y) {
   for (int64_t m = 0; m < M; ++m)
@@ -415,6 +419,11 @@ void oracle_fused_epilogue(const int32_t* acc, const float* sx, const float* ws,
       float v = (float)acc[m * N + n];
       v = v * sx[m];
       v = v * ws[n];
+      if (r == 0) {
+        if (bias) v = v + bf16_to_f32(bias[n]);
+        y[m * N + n] = oracle_f32_to_bf16(v);
+        continue;
+      }
       double s = (double)v;
       for (int64_t j = 0; j < r; ++j) s += (double)bf16_to_f32(u[m * r + j]) * (double)bf16_to_f32(up[n * r + j]);
       if (bias) s += (double)bf16_to_f32(bias[n]);

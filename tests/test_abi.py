@@ -106,11 +106,29 @@ def test_split_planner_follows_the_measured_cost_models(lib):
     with its finishing pass (M=2048, N=K=5120: 65 against 85 us), a split where the tiles would leave three quarters
     of the CUs idle (M=512, N=4096, K=5120), a peel of the rows that would leave the last round a tenth full
     (M=3584, N=K=5120: 115 against 127 us), and whole tiles for the headline shape, whose 7680 tiles fill 30 rounds."""
-    assert lib.hf_int8_linear_ws_bytes(2048, 5120, 5120) == 0
-    assert lib.hf_int8_linear_ws_bytes(512, 4096, 5120) > 0
-    assert lib.hf_int8_linear_ws_bytes(3584, 5120, 5120) > 0
-    assert lib.hf_int8_linear_ws_bytes(32768, 15360, 5120) == 0
-    assert lib.hf_int8_linear_ws_bytes(37710, 5376, 14336) > 0  # the model's down projection: peeled
+    assert lib.hf_int8_linear_ws_bytes(2048, 5120, 5120, 0, 0) == 0
+    assert lib.hf_int8_linear_ws_bytes(512, 4096, 5120, 0, 0) > 0
+    assert lib.hf_int8_linear_ws_bytes(3584, 5120, 5120, 0, 0) > 0
+    assert lib.hf_int8_linear_ws_bytes(32768, 15360, 5120, 64, 0) == 0
+    assert lib.hf_int8_linear_ws_bytes(37710, 5376, 14336, 64, 0) > 0  # the model's down projection: peeled
+
+
+def test_workspace_queries_report_what_the_route_uses(lib):
+    """The size queries follow the kernel route the call takes: no workspace for the one-pass few-row kernel
+    (M <= 64 with 32-row weight slices on a quarter to one round of CUs) or for the 256 x 128 tiles (config 1's
+    layer), the split plan's partial planes otherwise; the 256 x 128 tiles cover rank <= 64 without SwiGLU, so the
+    same sizes with rank 96 or SwiGLU take the split path and report its planes."""
+    assert lib.hf_int8_linear_ws_bytes(64, 5120, 5120, 32, 0) == 0  # one pass
+    assert lib.hf_int8_linear_ws_bytes(17, 2048, 4096, 16, 1) == 0  # one pass, tanh-GELU
+    assert lib.hf_int8_linear_ws_bytes(1024, 3072, 3072, 32, 0) == 0  # 256 x 128 tiles
+    assert lib.hf_int8_linear_ws_bytes(1024, 3072, 3072, 96, 0) > 0
+    assert lib.hf_int8_linear_ws_bytes(1024, 3072, 3072, 32, 2) > 0  # SwiGLU
+    assert lib.hf_int8_linear_ws_bytes(256, 30720, 5120, 32, 0) == 0  # 256 x 128 tiles
+    assert lib.hf_int8_linear_ws_bytes(64, 30720, 5120, 32, 0) > 0  # 960 slices: more than one round, split
+    # the whole layer adds the low-rank projection's split partials (or needs nothing more)
+    assert lib.hf_convrot_linear_ws_bytes(64, 5120, 5120, 32, 0) == 0
+    assert 0 < lib.hf_convrot_linear_ws_bytes(2241, 3072, 14336, 32, 0) <= lib.hf_convrot_linear_noalloc_max_bytes()
+    assert lib.hf_convrot_linear_ws_bytes(2048, 5120, 14336, 32, 0) > lib.hf_convrot_linear_noalloc_max_bytes()
 
 
 def test_ceilings_library_loads_and_rejects_bad_arguments():

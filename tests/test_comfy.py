@@ -51,7 +51,7 @@ def write(path, tensors, metadata):
     save_file(tensors, str(path), metadata=metadata)
 
 
-def comfy_file(tmp_path, fmt=1, scalar_scale=False, tag="int8_tensorwise"):
+def comfy_file(tmp_path, fmt=1, scalar_scale=False, tag="int8_tensorwise", group=None):
     gen = torch.Generator().manual_seed(7)
     d, ffn = 64, 96
     t = {}
@@ -71,7 +71,8 @@ def comfy_file(tmp_path, fmt=1, scalar_scale=False, tag="int8_tensorwise"):
     t["blocks.1.mlp.fc2.up.weight"] = (torch.randn(d, 16, generator=gen) * 0.02).to(torch.bfloat16)
     t["final_norm.weight"] = torch.ones(d)
     path = tmp_path / "model.safetensors"
-    write(path, t, {"hyperflow": json.dumps({"format": fmt})})
+    meta = {"format": fmt} if group is None else {"format": fmt, "convrot_group": group}
+    write(path, t, {"hyperflow": json.dumps(meta)})
     return path, t
 
 
@@ -80,18 +81,18 @@ def test_metadata_check(tmp_path):
     assert check_metadata(str(path))["format"] == 1
     plain = tmp_path / "plain.safetensors"
     write(plain, {"w": torch.zeros(2)}, {})
-    with pytest.raises(RuntimeError, match="not a HyperFlow checkpoint"):
+    with pytest.raises(RuntimeError, match="no 'hyperflow' entry"):
         check_metadata(str(plain))
     future = tmp_path / "future.safetensors"
     write(future, {"w": torch.zeros(2)}, {"hyperflow": json.dumps({"format": 2})})
-    with pytest.raises(RuntimeError, match="layout 2"):
+    with pytest.raises(RuntimeError, match="format 2"):
         check_metadata(str(future))
 
 
 def test_block_linears_land_on_the_reference_names(tmp_path):
     path, t = comfy_file(tmp_path)
     model = Toy()
-    done = load_comfy_checkpoint(model, str(path), group=16)
+    done = load_comfy_checkpoint(model, str(path), group=16, rotated=True)
     b0, b1 = model.transformer_blocks
     assert sorted(done["int8"]) == ["transformer_blocks.0.attn.to_q", "transformer_blocks.1.attn.to_out.0",
                                     "transformer_blocks.1.ff.net.0.proj"]
@@ -111,7 +112,7 @@ def test_gated_projection_halves_follow_the_reference_order(tmp_path):
     ComfyUI's silu(gate) * hidden of the file's own row order."""
     path, t = comfy_file(tmp_path)
     model = Toy()
-    load_comfy_checkpoint(model, str(path), group=16)
+    load_comfy_checkpoint(model, str(path), group=16, rotated=True)
     proj = model.transformer_blocks[1].ff.net[0].proj
     comfy = Int8RotLinear(64, 192, 16, activation="swiglu_gate_first")
     comfy.qweight.copy_(t["blocks.1.mlp.fc1.weight"])
@@ -129,12 +130,29 @@ def test_gated_projection_halves_follow_the_reference_order(tmp_path):
 def test_scalar_scale_is_broadcast_and_format_tag_checked(tmp_path):
     path, _ = comfy_file(tmp_path, scalar_scale=True)
     model = Toy()
-    load_comfy_checkpoint(model, str(path), group=16)
+    load_comfy_checkpoint(model, str(path), group=16, rotated=True)
     ws = model.transformer_blocks[1].attn.to_out[0].wscale
     assert ws.shape == (64,) and torch.all(ws == torch.tensor(3e-3, dtype=torch.float32))
     other = tmp_path / "other"
     other.mkdir()
     path2, _ = comfy_file(other, tag="fp8_tensorwise")
     with pytest.raises(ValueError, match="int8_tensorwise"):
-        load_comfy_checkpoint(Toy(), str(path2), group=16)
+        load_comfy_checkpoint(Toy(), str(path2), group=16, rotated=True)
     assert decode_comfy_quant(quant_tag()) == {"format": "int8_tensorwise"}
+
+
+def test_int8_parts_need_a_stated_rotation_basis(tmp_path):
+    """Int8RotLinear rotates its input, so INT8 weights load only when the file's metadata names their Hadamard group
+    or the caller vouches for it; low-rank parts alone load either way."""
+    path, t = comfy_file(tmp_path)
+    with pytest.raises(ValueError, match="rotated=True"):
+        load_comfy_checkpoint(Toy(), str(path), group=16)
+    named = tmp_path / "named"
+    named.mkdir()
+    path2, _ = comfy_file(named, group=16)
+    model = Toy()
+    done = load_comfy_checkpoint(model, str(path2), group=16)
+    assert len(done["int8"]) == 3
+    assert torch.equal(model.transformer_blocks[0].attn.to_q.qweight, t["blocks.0.attn.q_proj.weight"])
+    with pytest.raises(ValueError, match="group 16, loader asked for 64"):
+        load_comfy_checkpoint(Toy(), str(path2), group=64)

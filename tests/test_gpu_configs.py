@@ -28,7 +28,7 @@ import numpy as np
 import pytest
 import torch
 
-from golden_utils import within_fp32_sum_bound
+from golden_utils import check_against_composition, device_lowrank_slack, within_fp32_sum_bound
 
 pytestmark = pytest.mark.gpu
 
@@ -114,8 +114,11 @@ def check_layer(lib, layer, x: torch.Tensor, y: torch.Tensor, rows: np.ndarray) 
     got = lib.bf16_to_f32(got_bits)
     want = lib.bf16_to_f32(fused)
     assert (np.abs(got - want) <= np.abs(want) * 2.0**-7 + 1e-6).all()
-    comp = lib.bf16_to_f32(lib.composition(out["y"], xb, down, up, bias))
-    assert np.abs(got - comp).max() / np.abs(comp).max() <= 1e-2
+    # against the reference's composition Int8RotLinear(x) + LowRankLinear(x) + bias, elementwise
+    lowrank = lib.lowrank_up(u_ref, up) if layer.rank else None
+    extra = device_lowrank_slack(xb, down, u_ref, up, out["y"], bias) if layer.rank else None
+    check_against_composition(got_bits, out["y"], lowrank, bias, lib.composition(out["y"], xb, down, up, bias),
+                              extra=extra)
 
 
 def check_gelu(lib, fused_act: torch.Tensor, pre: torch.Tensor, rows: np.ndarray) -> None:

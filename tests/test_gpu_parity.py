@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 import torch
 
-from golden_utils import classify_rotation_mismatches, fixture_names, load_fixture, within_fp32_sum_bound
+from golden_utils import (check_against_composition, classify_rotation_mismatches, device_lowrank_slack, fixture_names,
+                          load_fixture, within_fp32_sum_bound)
 
 pytestmark = pytest.mark.gpu
 
@@ -275,9 +276,11 @@ def test_lowrank_bias_extension_against_the_reference_composition(oracle_lib):
         layer.bias.copy_(to_dev_bf16(f["bias"]))
         y = layer(to_dev_bf16(f["x"]))
     got = oracle_lib.bf16_to_f32(bits_of(y))
-    comp = oracle_lib.bf16_to_f32(f["y_composed"])
-    tolerance = 1e-2  # max |y - y_ref| / max |y_ref| against the reference's bf16 composition
-    assert np.abs(got - comp).max() / np.abs(comp).max() <= tolerance
+    # against the reference's bf16 composition (written by its modules), elementwise: every element within the
+    # composition's rounding bound plus the device's fp32 summation slack, >= 99.5 % within one bf16 step, and
+    # max |y - y_ref| / max |y_ref| <= 1e-2
+    extra = device_lowrank_slack(f["x"], f["down"], f["u"], f["up"], f["y"], f["bias"])
+    check_against_composition(bits_of(y), f["y"], f["lowrank"], f["bias"], f["y_composed"], extra=extra)
     # against the fused definition (fp32 sum, one rounding): within one bf16 ulp, elementwise
     out = oracle_lib.convrot_linear(f["x"], f["qweight"], f["wscale"], f["G"])
     u = oracle_lib.lowrank_down(f["x"], f["down"])

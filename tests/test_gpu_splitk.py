@@ -50,7 +50,7 @@ def run_linear(lib, q, w, sx, ws, u, up, bias, split):
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     args = (p(q), k, p(w), k, p(sx), p(ws), p(u), r if r else 0, p(up), r if r else 0, r, p(bias), p(y), n, m, n, k)
     if split:
-        nbytes = lib.hf_int8_linear_ws_bytes(m, n, k)
+        nbytes = lib.hf_int8_linear_ws_bytes(m, n, k, r, 0)
         assert nbytes > 0, "this shape should take the split path"
         work = torch.empty(nbytes, device=DEV, dtype=torch.uint8)
         status = lib.hf_int8_linear_ws(*args, p(work), nbytes, stream)
@@ -61,14 +61,14 @@ def run_linear(lib, q, w, sx, ws, u, up, bias, split):
     return y
 
 
-@pytest.mark.parametrize("m,n,k,r,bias", [(1, 5120, 5120, 0, False), (64, 5120, 5120, 0, False),
-                                          (64, 5000, 5120, 32, True), (200, 3072, 3072, 64, False),
+@pytest.mark.parametrize("m,n,k,r,bias", [(1, 30720, 5120, 0, False), (64, 16384, 2048, 0, False),
+                                          (64, 15000, 5120, 32, True), (200, 3072, 3072, 64, False),
                                           (37, 1000, 2048, 136, True), (256, 5120, 5120, 32, False),
                                           (100, 3000, 3072, 32, True), (128, 30720, 1024, 0, False),
                                           (256, 8192, 2048, 0, False),
                                           # K a multiple of 16 but not of the 128-byte stage: partial last stages
-                                          (64, 4096, 1040, 0, False), (200, 2048, 2064, 0, False),
-                                          (256, 3072, 1040, 32, True), (17, 5000, 2064, 8, False)])
+                                          (64, 12288, 1040, 0, False), (200, 2048, 2064, 0, False),
+                                          (256, 3072, 1040, 32, True), (17, 10000, 2064, 8, False)])
 def test_split_gemm_is_bitwise_the_unsplit_gemm(oracle_lib, m, n, k, r, bias):
     from hyperflow_h3_flash_amd import _native
     from hyperflow_h3_flash_amd.int8 import rotate_quant
@@ -174,7 +174,7 @@ def test_large_shapes_do_not_split():
     from hyperflow_h3_flash_amd import _native
 
     lib = _native.library()
-    assert lib.hf_int8_linear_ws_bytes(32768, 15360, 5120) == 0
+    assert lib.hf_int8_linear_ws_bytes(32768, 15360, 5120, 64, 0) == 0
     assert lib.hf_lowrank_down_ws_bytes(32768, 5120, 64) == 0
 
 
@@ -191,7 +191,7 @@ def test_trailing_tile_rows_split_is_bitwise_the_whole_gemm(oracle_lib, m, n, k,
     from hyperflow_h3_flash_amd import _native
 
     lib = _native.library()
-    nbytes = lib.hf_int8_linear_ws_bytes(m, n, k)
+    nbytes = lib.hf_int8_linear_ws_bytes(m, n, k, r, act)
     assert nbytes > 0, "the trailing tile rows should take the split path"
     gen = torch.Generator(device=DEV).manual_seed(m + n + k)
     q = torch.randint(-127, 128, (m, k), device=DEV, dtype=torch.int8, generator=gen)

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 import torch
 
-from golden_utils import fixture_names, load_fixture
+from golden_utils import check_against_composition, fixture_names, load_fixture
 from hyperflow_h3_flash_amd import Int8RotLinear, LowRankLinear, host, regular_hadamard
 from hyperflow_h3_flash_amd import int8 as int8_mod
 
@@ -67,9 +67,8 @@ def test_host_fused_extension_against_the_reference_composition(oracle_lib):
         layer.up.weight.copy_(bf16_tensor(f["up"]))
         layer.bias.copy_(bf16_tensor(f["bias"]))
         y = layer(bf16_tensor(f["x"]))
-    got = oracle_lib.bf16_to_f32(bits_of(y))
-    comp = oracle_lib.bf16_to_f32(f["y_composed"])
-    assert np.abs(got - comp).max() / np.abs(comp).max() <= 1e-2  # the fused extension's bar
+    # the fused extension's bar against the reference's composition, elementwise
+    check_against_composition(bits_of(y), f["y"], f["lowrank"], f["bias"], f["y_composed"])
     # the fused definition (fp32 dequantization, exact low-rank sum and bias, one rounding): bitwise
     u = host.lowrank_down(bf16_tensor(f["x"]), bf16_tensor(f["down"]))
     np.testing.assert_array_equal(bits_of(u), f["u"])  # the reference's bf16 nn.Linear intermediate

@@ -58,7 +58,7 @@ def run(lib, c, noalloc: bool, act: int = 0):
     if noalloc:
         status = lib.hf_convrot_linear_noalloc(*head, stream)
     else:
-        nbytes = lib.hf_convrot_linear_ws_bytes(m, n, k, r)
+        nbytes = lib.hf_convrot_linear_ws_bytes(m, n, k, r, act)
         work = torch.empty(max(nbytes, 1), device=DEV, dtype=torch.uint8)
         status = lib.hf_convrot_linear_ws(*head, p(work) if nbytes else None, nbytes, stream)
     assert status == 0, status
@@ -66,12 +66,14 @@ def run(lib, c, noalloc: bool, act: int = 0):
     return y.view(torch.int16).cpu().numpy()
 
 
-# (m, k, n, rank, bias, activation): split-K tile GEMMs, the skinny kernel with the row-wise low-rank launch, SwiGLU
-# in pair order; each pair runs the larger shape first.
+# (m, k, n, rank, bias, activation), every call using the scratch: the split low-rank down projection ahead of the
+# 256 x 128 tiles, then the skinny kernel's K split; the skinny K split at 256 and at 64 rows (too many weight slices
+# for the one-pass kernel); SwiGLU in pair order, then tanh-GELU, both split over K. Each pair runs the larger input
+# first.
 PAIRS = [
     ((1024, 5120, 5120, 32, True, 0), (300, 3072, 3072, 64, False, 0)),
-    ((256, 5120, 15360, 32, False, 0), (64, 5120, 5120, 32, True, 0)),
-    ((200, 5376, 14336, 64, True, 2), (17, 2048, 4096, 16, False, 1)),
+    ((256, 5120, 15360, 32, False, 0), (64, 5120, 30720, 32, True, 0)),
+    ((200, 5376, 14336, 64, True, 2), (17, 2048, 16384, 16, False, 1)),
 ]
 
 
@@ -83,7 +85,7 @@ def test_noalloc_matches_the_workspace_entry_point_twice(first, second):
     limit = lib.hf_convrot_linear_noalloc_max_bytes()
     for i, (m, k, n, r, bias, act) in enumerate((first, second)):
         print(f"noalloc call {i}: M={m} K={k} N={n} r={r} bias={bias} act={act}", flush=True)
-        need = lib.hf_convrot_linear_ws_bytes(m, n, k, r)
+        need = lib.hf_convrot_linear_ws_bytes(m, n, k, r, act)
         assert 0 < need <= limit, "the case should use the scratch"
         c = case(m, k, n, r, bias, seed=m + n + i)
         got = run(lib, c, True, act)
@@ -97,7 +99,7 @@ def test_noalloc_refuses_calls_beyond_its_scratch():
 
     lib = _native.library()
     m, k, n, r = 2048, 14336, 5120, 32  # split over K: 126 MB of int32 partial planes
-    assert lib.hf_convrot_linear_ws_bytes(m, n, k, r) > lib.hf_convrot_linear_noalloc_max_bytes()
+    assert lib.hf_convrot_linear_ws_bytes(m, n, k, r, 0) > lib.hf_convrot_linear_noalloc_max_bytes()
     c = case(8, k, n, r, False, seed=1)  # the buffers are never touched: the size check comes first
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     status = lib.hf_convrot_linear_noalloc(p(c["x"]), k, None, None, 0, 0, p(c["w"]), k, p(c["ws"]), p(c["down"]), k,
