@@ -108,8 +108,10 @@ def copy_probe(torch):
 def ceilings(torch, repeats=5):
     """Measured ceilings of this device, beside the published peaks: the INT8 matrix cores' rate with no memory
     traffic (libhf_ceilings.so, one 8-wave workgroup per CU issuing independent v_mfma_i32_32x32x32_i8) on zero
-    operands and on uniform random codes, whose bit toggling sets the clock the chip holds, and the bandwidth of a
-    1 GiB device-to-device copy (read + write bytes). Each figure is the mean of `repeats` launches after two."""
+    operands and on uniform random codes, whose bit toggling sets the clock the chip holds, the bandwidth of a
+    1 GiB device-to-device copy (read + write bytes), and of streaming passes over 1 GiB (libhf_ceilings.so
+    stream_kernel) at the rotation's 2:1 read:write ratio and read-only, the best of a sweep of launch shapes. Each
+    figure is the mean of `repeats` launches after two."""
     from hyperflow_h3_flash_amd import _native
 
     lib = _native.ceilings_library()
@@ -146,7 +148,23 @@ def ceilings(torch, repeats=5):
     dst = torch.empty_like(src)
     t = mean_seconds(lambda: dst.copy_(src))
     result["copy_GBs"] = round(2.0 * src.numel() * 4 / t / 1e9, 1)
-    del src, dst
+    # Streaming passes over 1 GiB of source (libhf_ceilings.so stream_kernel), the best of a sweep of grid sizes
+    # and unrolls: 2 bytes read per byte written (the rotation's ratio), read-only (the low-rank projection's).
+    units = (1 << 30) // 32
+    sink = torch.empty(cus * 16 * 256, dtype=torch.int32, device=dev)
+    for name, (reads, writes) in {"stream_r2w1_GBs": (2, 1), "stream_read_GBs": (2, 0)}.items():
+        best = 0.0
+        for grid in (cus * 2, cus * 4, cus * 8, cus * 16):
+            for unroll in (4, 8):
+                def launch():
+                    rc = lib.hf_ceiling_stream(src.data_ptr(), dst.data_ptr() if writes else None, units, reads,
+                                               writes, unroll, grid, sink.data_ptr(), stream.cuda_stream)
+                    if rc != 0:
+                        raise RuntimeError(f"hf_ceiling_stream failed: {rc}")
+                t = mean_seconds(launch)
+                best = max(best, units * 16 * (reads + writes) / t / 1e9)
+        result[name] = round(best, 1)
+    del src, dst, sink
     return result
 
 
@@ -373,6 +391,7 @@ def main():
         "pct_of_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
         "kernel_us": {k: round(v, 2) for k, v in avg_us.items()},
         "rotate_quant_GBs": round(rotate_bytes / (avg_us["rotate"] * 1e-6) / 1e9, 1),
+        "lowrank_down_GBs": round((2 * M * K + 2 * M * RANK) / (avg_us["lowrank"] * 1e-6) / 1e9, 1),
         "roofline": {
             "bound": "mfma",
             "achieved": round(gemm_tops, 2),
@@ -388,6 +407,8 @@ def main():
     ceil = ceilings(torch)
     ceil["gemm_frac_of_mfma_uniform"] = round(gemm_tops / ceil["mfma_int8_uniform_TOPS"], 4)
     ceil["rotate_quant_frac_of_copy"] = round(result["rotate_quant_GBs"] / ceil["copy_GBs"], 4)
+    ceil["rotate_quant_frac_of_stream"] = round(result["rotate_quant_GBs"] / ceil["stream_r2w1_GBs"], 4)
+    ceil["lowrank_down_frac_of_stream"] = round(result["lowrank_down_GBs"] / ceil["stream_read_GBs"], 4)
     result["ceilings"] = ceil
     if not args.no_cpu_baseline:
         del x, layer

@@ -128,6 +128,8 @@ def ceilings_library() -> ctypes.CDLL:
     lib.hf_ceiling_mfma_i8.restype = ctypes.c_int
     lib.hf_ceiling_mfma_i8_macs.argtypes = [_I32, _I32]
     lib.hf_ceiling_mfma_i8_macs.restype = ctypes.c_int64
+    lib.hf_ceiling_stream.argtypes = [_P, _P, _I64, _I32, _I32, _I32, _I32, _P, _P]
+    lib.hf_ceiling_stream.restype = ctypes.c_int
     return lib
 
 

@@ -142,3 +142,10 @@ def test_ceilings_library_loads_and_rejects_bad_arguments():
     assert lib.hf_ceiling_mfma_i8(None, 1, 1, buf, None) == -1
     assert lib.hf_ceiling_mfma_i8(buf, 0, 1, buf, None) == -1
     assert lib.hf_ceiling_mfma_i8(buf, 1, 0, buf, None) == -1
+    # the streaming ceiling: units a multiple of 64, a supported (reads, writes) pair and unroll, buffers present
+    assert lib.hf_ceiling_stream(buf, buf, 100, 2, 1, 4, 1, buf, None) == -1
+    assert lib.hf_ceiling_stream(buf, buf, 64, 3, 1, 4, 1, buf, None) == -1
+    assert lib.hf_ceiling_stream(buf, buf, 64, 2, 1, 6, 1, buf, None) == -1
+    assert lib.hf_ceiling_stream(buf, None, 64, 2, 1, 4, 1, buf, None) == -1
+    assert lib.hf_ceiling_stream(buf, None, 64, 2, 0, 4, 1, None, None) == -1
+    assert lib.hf_ceiling_stream(None, buf, 64, 1, 1, 4, 1, buf, None) == -1
