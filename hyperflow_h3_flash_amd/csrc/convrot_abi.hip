@@ -311,6 +311,27 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
     plan = LrPlan{};  // no (or too small a) workspace: one pass over K
     plan.k_chunk = (int)K;
   }
+  if (plan.splits == 1 && r >= 192 && aligned(u, 16) && (ldu % 8) == 0 &&
+      2 * ((M + hf::GBM - 1) / hf::GBM) * ((r + hf::GBN - 1) / hf::GBN) >= device_cus()) {
+    // Wide ranks with many rows: the persistent 256 x 256 tiles' bf16 product (x rows against down rows, K in
+    // bytes), one pass over x per 256 ranks with the matrix cores at the tile kernel's rate. The summation order
+    // (64-element stages, 16-element MFMA steps, K ascending) is lowrank_down_wide_kernel's.
+    hf::GemmArgs a{};
+    a.q = reinterpret_cast<const int8_t*>(x); a.ldq = 2 * ldx;
+    a.w = reinterpret_cast<const int8_t*>(down); a.ldw = 2 * ld_down;
+    a.out = u; a.ldo = ldu;
+    a.M = (int)M; a.N = r; a.K = (int)(2 * K); a.out_vec16 = 1;
+    a.tiles_m = (int)((M + hf::GBM - 1) / hf::GBM);
+    a.tiles_n = (int)((r + hf::GBN - 1) / hf::GBN);
+    a.splits = 1;
+    a.k_chunk = (int)((a.K + hf::GBK - 1) / hf::GBK * hf::GBK);
+    if ((int64_t)hf::GBM * a.ldq >= (int64_t(1) << 32) || (int64_t)hf::GBN * a.ldw >= (int64_t(1) << 32))
+      return HF_ERR_SIZE;
+    const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+    hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutMmBf16>, dim3((unsigned)gemm_grid(tiles)), dim3(hf::kThreads),
+                       hf::kGemmLds, s, a);
+    return launch_status();
+  }
   if (plan.splits == 1 && r > hf::kLrRanks) {
     // Ranks past 64 with many rows: 256 ranks per pass over x (lowrank_down_wide_kernel), 4 or 5 row blocks of 32
     // per workgroup (5 when 128-row workgroups would need more than one round of CUs).
@@ -561,6 +582,17 @@ GemmRoute gemm_route(int64_t M, int64_t N, int64_t K, int32_t r, bool glu) {
 
 bool is_glu(int act_code) { return act_code == HF_ACT_SWIGLU || act_code == HF_ACT_SWIGLU_GATE_FIRST; }
 
+// Whether the low-rank up projection runs on the persistent 256 x 256 tiles (int8_gemm_kernel's bf16 product): its
+// output fills at least one round of them. Its K (the rank) is small, so the output (2 bytes per element) and the
+// operand rows re-read per tile are the traffic; 256 x 256 tiles read 4 operand bytes per output element against
+// 8 for the 128 x 128 tiles of lowrank_up_kernel, and their stores leave the CU as whole lines behind the next
+// tile's loads. From rank 128: at M=37710 the up projection to N=7168 took 180-220 us on the tiles against 207-270
+// us at rank 256, but 120-140 against 112-120 us at rank 64, where a tile's two stages (one of them zeros) are too
+// short for the persistent pipeline to pay.
+bool use_up_tiles(int64_t M, int64_t N, int32_t r) {
+  return r >= 128 && ((M + hf::GBM - 1) / hf::GBM) * ((N + hf::GBN - 1) / hf::GBN) >= device_cus();
+}
+
 int64_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r, int act_code) {
   if (M <= 0 || N <= 0 || K <= 0 || r < 0) return 0;
   return gemm_route(M, N, K, r, is_glu(act_code)).ws_bytes;
@@ -796,9 +828,27 @@ int hf_lowrank_up(const uint16_t* u, int64_t ldu, const uint16_t* up, int64_t ld
   if (M >= (int64_t(1) << 31) || N >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   if (2 * hf::kUpTile * std::max(ldu, ld_up) >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   allow_large_lds();
+  const int vec16 = aligned(y, 16) && (ldy % 8) == 0;
+  if (vec16 && use_up_tiles(M, N, r)) {
+    // At least a round of 256 x 256 output tiles: the persistent tile kernel's bf16 product (kOutMmBf16), the
+    // operands' rows as bytes (2r bytes of rank per row).
+    hf::GemmArgs a{};
+    a.q = reinterpret_cast<const int8_t*>(u); a.ldq = 2 * ldu;
+    a.w = reinterpret_cast<const int8_t*>(up); a.ldw = 2 * ld_up;
+    a.bias = bias; a.out = y; a.ldo = ldy;
+    a.M = (int)M; a.N = (int)N; a.K = 2 * r; a.out_vec16 = 1;
+    a.tiles_m = (int)((M + hf::GBM - 1) / hf::GBM);
+    a.tiles_n = (int)((N + hf::GBN - 1) / hf::GBN);
+    a.splits = 1;
+    a.k_chunk = (int)((a.K + hf::GBK - 1) / hf::GBK * hf::GBK);
+    const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+    if (tiles >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+    hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutMmBf16>, dim3((unsigned)gemm_grid(tiles)), dim3(hf::kThreads),
+                       hf::kGemmLds, static_cast<hipStream_t>(stream), a);
+    return launch_status();
+  }
   const int64_t tiles_n = (N + hf::kUpTile - 1) / hf::kUpTile, tiles = ((M + hf::kUpTile - 1) / hf::kUpTile) * tiles_n;
   if (tiles >= (int64_t(1) << 31)) return HF_ERR_SIZE;
-  const int vec16 = aligned(y, 16) && (ldy % 8) == 0;
   hipLaunchKernelGGL(hf::lowrank_up_kernel, dim3((unsigned)tiles), dim3(hf::kUpThreads), hf::kUpLds,
                      static_cast<hipStream_t>(stream), u, ldu, up, ld_up, bias, y, ldy, (int)M, (int)N, (int)r,
                      (int)tiles_n, vec16);

@@ -224,12 +224,24 @@ __device__ __forceinline__ void read_frags(Frags& f, const unsigned char HF_LDS*
   for (int ib = 0; ib < NB; ++ib) f.b[ib] = *(const v4i HF_LDS*)(Bs + ib * 32 * GBK);
 }
 
+// BF16 = false: the INT8 product (v_mfma_i32_32x32x32_i8, int32 sums). BF16 = true: the operands are bf16 and the
+// sums fp32 (v_mfma_f32_32x32x16_bf16, kept in the same registers): its fragment of a 32-byte K step is the same 16
+// bytes per lane (lane half h: elements 8h .. 8h + 7 of the step's 16) and its 32 x 32 result has the same layout.
+template <bool BF16 = false>
 __device__ __forceinline__ void mma(v16i (&acc)[NB][4], const Frags& f) {
 #pragma unroll
   for (int ib = 0; ib < NB; ++ib)
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
-      acc[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[ib], f.a[jb], acc[ib][jb], 0, 0, 0);
+    for (int jb = 0; jb < 4; ++jb) {
+      if constexpr (BF16) {
+        acc[ib][jb] = __builtin_bit_cast(
+            v16i, __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, f.b[ib]),
+                                                          __builtin_bit_cast(v8bf, f.a[jb]),
+                                                          __builtin_bit_cast(v16f, acc[ib][jb]), 0, 0, 0));
+      } else {
+        acc[ib][jb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[ib], f.a[jb], acc[ib][jb], 0, 0, 0);
+      }
+    }
 }
 
 #define HF_BARRIER() asm volatile("s_barrier" ::: "memory")
@@ -249,8 +261,10 @@ __device__ __forceinline__ void wait_vm(int n) {
 }
 
 // Output modes: int32 accumulators; bf16 with the dequantization (and, for r > 64, the low-rank term from global
-// memory) and bias; bf16 with a rank <= 64 low-rank term whose operands ride the ring.
-constexpr int kOutI32 = 0, kOutBf16 = 1, kOutBf16Lr = 2;
+// memory) and bias; bf16 with a rank <= 64 low-rank term whose operands ride the ring; and kOutMmBf16, a bf16
+// product: q and w hold bf16 rows (ldq, ldw and K in bytes), the sums are fp32 and the output is bf16(sum + bias)
+// (the low-rank up projection, whose small K and large output suit the persistent tiles and their whole-line stores).
+constexpr int kOutI32 = 0, kOutBf16 = 1, kOutBf16Lr = 2, kOutMmBf16 = 3;
 
 
 // Persistent kernel: one workgroup per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... Every wave issues the
@@ -303,7 +317,7 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   // MFMA, and, when `loads` issues a stage's loads, those two per MFMA after them.
   auto kstep = [&](const Frags& use, auto&& read, auto&& loads) {
     read();
-    mma(acc, use);
+    mma<OUT == kOutMmBf16>(acc, use);
     loads();
 #pragma unroll
     for (int i = 0; i < (4 + NB) / 2; ++i) {
@@ -344,12 +358,17 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       const int mr = min(cur.m0 + pt, a.M - 1);
       const int ncol = min(cur.n0 + pt, a.N - 1);
       const int nc = kGlu ? glu_row(ncol, a.glu_half, a.glu_gate_first) : ncol;
-      const uint16_t* bsrc = a.bias ? a.bias : reinterpret_cast<const uint16_t*>(a.sw);
-      if (kThreads == 256 || threadIdx.x < 256) {
-        p_val = a.sx[mr];
-        p_ws = a.sw[nc];
+      if constexpr (OUT == kOutMmBf16) {
+        // A bf16 product has no scales; the bias is optional.
+        if ((kThreads == 256 || threadIdx.x >= 256) && a.bias) p_bias = (uint32_t)a.bias[nc];
+      } else {
+        const uint16_t* bsrc = a.bias ? a.bias : reinterpret_cast<const uint16_t*>(a.sw);
+        if (kThreads == 256 || threadIdx.x < 256) {
+          p_val = a.sx[mr];
+          p_ws = a.sw[nc];
+        }
+        if (kThreads == 256 || threadIdx.x >= 256) p_bias = (uint32_t)bsrc[nc];
       }
-      if (kThreads == 256 || threadIdx.x >= 256) p_bias = (uint32_t)bsrc[nc];
     }
 
 #pragma unroll
@@ -495,7 +514,10 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
               const int nl = wn * WN + ib * 32 + 8 * (v >> 2) + 4 * ehalf + (v & 3);
-              c[i2][jb][v] = ((float)acc[ib][jb][v] * sxv[jb]) * params[256 + nl];
+              if constexpr (OUT == kOutMmBf16)
+                c[i2][jb][v] = __int_as_float(acc[ib][jb][v]);  // the fp32 sum
+              else
+                c[i2][jb][v] = ((float)acc[ib][jb][v] * sxv[jb]) * params[256 + nl];
             }
         }
         if constexpr (kLr) {
@@ -726,5 +748,6 @@ template __global__ void int8_gemm_kernel<kOutBf16, kActGeluTanh>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16Lr, kActGeluTanh>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16, kActSwiGLU>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16Lr, kActSwiGLU>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutMmBf16>(GemmArgs);  // bf16 product (the low-rank up projection)
 
 }  // namespace hf

@@ -10,6 +10,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
+from golden_utils import within_fp32_sum_bound
 
 pytestmark = pytest.mark.gpu
 
@@ -50,6 +51,35 @@ def test_lowrank_up_matches_oracle(oracle_lib, m, n, r, bias):
     y = lowrank_up(to_dev_bf16(u), to_dev_bf16(up), None if b is None else to_dev_bf16(b))
     ok, exact = within_one_ulp(bits_of(y), oracle_lib.lowrank_up(u, up, b), oracle_lib)
     assert ok and exact > 0.98
+
+
+@pytest.mark.parametrize("m,n,r,bias", [(4096, 4096, 256, False), (4100, 4200, 136, True), (2048, 8448, 512, True),
+                                        (4096, 4096, 128, False)])
+def test_lowrank_up_on_the_persistent_tiles_matches_oracle(oracle_lib, m, n, r, bias):
+    """Ranks from 128 with at least one round of 256 x 256 output tiles take the persistent tile kernel's bf16
+    product (r=136: a K of 272 bytes, a partial last stage; r=128: two stages): sampled rows
+    (the first, the last and ragged tile edges included) within the error bound of an fp32 sum of the rank's products
+    of the oracle's exactly rounded sum, bitwise on almost every element, every row finite."""
+    from hyperflow_h3_flash_amd.int8 import lowrank_up
+
+    assert ((m + 255) // 256) * ((n + 255) // 256) >= 256  # the tile route at 256 CUs
+    gen = torch.Generator(device=DEV).manual_seed(m + n + r)
+    u = (torch.randn(m, r, device=DEV, generator=gen)).to(torch.bfloat16)
+    up = (torch.randn(n, r, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(n, device=DEV, generator=gen) * 0.01).to(torch.bfloat16) if bias else None
+    print(f"lowrank_up tiles M={m} N={n} r={r} bias={bias}", flush=True)
+    y = lowrank_up(u, up, b)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y.float()).all())
+    rows = np.unique(np.concatenate([[0, 255, 256], np.arange(m - 3, m),
+                                     np.random.default_rng(m).choice(m, size=12, replace=False)]))
+    u_rows = bits_of(u[torch.from_numpy(rows).to(DEV)])
+    want = oracle_lib.lowrank_up(u_rows, bits_of(up), None if b is None else bits_of(b))
+    got = oracle_lib.bf16_to_f32(bits_of(y[torch.from_numpy(rows).to(DEV)]))
+    ref = oracle_lib.bf16_to_f32(want)
+    # an fp32 sum of r products in any order, rounded once (a bias, when present, is one more exact term)
+    assert within_fp32_sum_bound(got, ref, oracle_lib.bf16_to_f32(u_rows), oracle_lib.bf16_to_f32(bits_of(up)))
+    assert (got == ref).mean() > 0.98
 
 
 def test_lowrank_linear_matches_the_reference_composition(oracle_lib):
@@ -153,14 +183,16 @@ def test_device_layer_without_the_library_raises(monkeypatch):
 
 
 @pytest.mark.parametrize("m,k,r", [(16500, 1040, 72), (20000, 5376, 256), (17000, 2048, 200), (33000, 1024, 320),
-                                   (33000, 1024, 512), (37710, 5376, 128)])
+                                   (33000, 1024, 512), (37710, 5376, 128), (37710, 5376, 256), (40000, 2064, 200)])
 def test_wide_rank_down_projection(oracle_lib, m, k, r):
     """Ranks past 64 with more rows than half the CUs' 128-row workgroups cover (no K split) take 256 ranks per pass
     over x (lowrank_down_wide_kernel): the same sums, in the same order, as 64-rank passes of the unsplit rank-64
     kernel (bitwise). Against the exact sums s (float64, sampled rows): bitwise the oracle's exactly rounded value on
     almost every element, and everywhere within the fp32 accumulation bound, |u - s| <= 2^-8 |s| + (1 + 2^-8) K
-    2^-24 sum_k |x_k d_k| (a sum that cancels to near zero can miss one bf16 ulp of itself). M=33000 and 37710 use
-    workgroups of five row blocks, and r=320 and 512 two passes."""
+    2^-24 sum_k |x_k d_k| (a sum that cancels to near zero can miss one bf16 ulp of itself). M=37710 with r=128 uses
+    workgroups of five row blocks. From r=192 with enough 256-row blocks to fill half the CUs (M=33000, r=320 and
+    512; M=37710, r=256; M=40000, r=200 with a partial column tile and K=2064, not a multiple of the 64-element
+    stage) the persistent tile kernel's bf16 product runs instead, with the same summation order."""
     from hyperflow_h3_flash_amd import _native
     from hyperflow_h3_flash_amd.int8 import _stream, lowrank_down
 
