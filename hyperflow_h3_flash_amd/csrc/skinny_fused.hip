@@ -4,9 +4,10 @@
 //   y[m, n] = bf16((f32(acc) * sx[m]) * sw[n] + sum_j u[m, j] * up[n, j] + bias[n]),   acc = q @ w^T exact int32.
 //
 // With few rows the weight stream is the traffic (N x K bytes against MR x K of codes that stay in L2), so each
-// workgroup takes a slice of 32 weight rows (N / 32 workgroups: 160 at N = 5120) and all MR code rows, streams the
-// slice's whole K through a deep LDS ring (D stages of 32 + MR rows x 128 bytes, LDS-DMA whole lines, D - 1 stages
-// in flight), and splits each 128-byte stage's four 32-byte K steps over its four waves. At the end the waves' int32
+// workgroup takes a slice of at most 32 weight rows (`rows`, chosen by the host so the slices cover every CU: 20 at
+// N = 5120 on 256 CUs; rows past the slice read as zero and their columns are not stored) and all MR code rows,
+// streams the slice's whole K through an LDS ring (D stages of 32 + MR rows x 128 bytes, LDS-DMA whole lines,
+// D - 1 stages in flight), and splits each 128-byte stage's four 32-byte K steps over its four waves. At the end the waves' int32
 // partial sums are added through LDS (exact in any order) and each 32 x 32 output block goes through the split-K
 // finishing pass's epilogue (block_load / block_finish), so the outputs are bitwise those of the split path and of
 // the tile GEMM. Against splitting K over workgroups, there are no int32 partial planes to write and read back and no
@@ -15,15 +16,17 @@
 
 namespace hf {
 
-constexpr int kSfN = 32;        // weight rows per workgroup
+constexpr int kSfN = 32;        // weight rows per workgroup, at most (the rows of a stage's weight part)
 constexpr int kSfWaves = 4;
 constexpr int kSfSub = 1;                 // 128-byte K pieces per stage (2 measured no faster)
 constexpr int kSfStageK = 128 * kSfSub;   // K bytes per stage
 // A stage holds kSfSub pieces, each (32 + mr) rows x 128 bytes laid out like one 128-byte stage.
 __host__ __device__ constexpr int sf_piece_bytes(int mr) { return (kSfN + mr) * 128; }
 __host__ __device__ constexpr int sf_stage_bytes(int mr) { return kSfSub * sf_piece_bytes(mr); }
-// Ring depth: as many stages as fit 144 KiB (12 with 64 code rows).
-__host__ __device__ constexpr int sf_depth(int mr) { return (144 * 1024) / sf_stage_bytes(mr); }
+// Ring depth: 8 stages (96 KiB with 64 code rows). Measured at M=64 (graph replays over weight copies, runtime slice
+// heights): 4, 6, 8 and 12 stages took 19.1, 18.5, 18.4 and 19.3 us at N=K=5120, 17.2, 16.4, 16.3 and 17.2 us at
+// N=4096, 36.0, 33.1, 32.6 and 33.6 us at M=48, K=14336, N=5376: past 8 the extra requests in flight only queue.
+__host__ __device__ constexpr int sf_depth(int mr) { return 8; }
 __host__ __device__ constexpr int sf_lds(int mr) { return sf_depth(mr) * sf_stage_bytes(mr); }
 
 template <int MR, bool GLU>
@@ -31,7 +34,7 @@ __global__ __launch_bounds__(64 * kSfWaves, 1) void skinny_fused_kernel(
     const int8_t* __restrict__ q, int64_t ldq, const int8_t* __restrict__ w, int64_t ldw, const float* __restrict__ sx,
     const float* __restrict__ sw, const uint16_t* __restrict__ u, int64_t ldu, const uint16_t* __restrict__ up,
     int64_t ldup, int r, const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K,
-    int vec, int act, int glu_half, int glu_gate_first) {
+    int vec, int act, int glu_half, int glu_gate_first, int rows) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char sf_smem_raw[];
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)sf_smem_raw;
   constexpr int kD = sf_depth(MR);
@@ -44,8 +47,9 @@ __global__ __launch_bounds__(64 * kSfWaves, 1) void skinny_fused_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane & 31, half = lane >> 5;
-  const int n0 = blockIdx.x * kSfN;
-  const int rows_n = min(kSfN, N - n0);
+  const int n0 = blockIdx.x * rows;
+  const int rows_n = min(rows, N - n0);
+  const int n_end = min(N, n0 + rows);  // this workgroup's columns end here (pair order: rows == 32)
   // Pair order scatters the slice's rows over both halves of the weight: one descriptor for all of it.
   const uint32_t bytes_w = (uint32_t)((GLU ? N : rows_n) * ldw), bytes_q = (uint32_t)(M * ldq);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w + (GLU ? 0 : (int64_t)n0 * ldw), bytes_w);
@@ -58,8 +62,8 @@ __global__ __launch_bounds__(64 * kSfWaves, 1) void skinny_fused_kernel(
 #pragma unroll
   for (int i = 0; i < kMine; ++i)
     if (wave + kSfWaves * i < kJB)
-      block_load(ops[i], 32 * (wave + kSfWaves * i), n0, sx, sw, u, ldu, up, ldup, r, bias, M, N, GLU, glu_half,
-                 glu_gate_first, lane);
+      block_load(ops[i], 32 * (wave + kSfWaves * i), n0, sx, sw, u, ldu, up, ldup, r, bias, M, GLU ? N : n_end, GLU,
+                 glu_half, glu_gate_first, lane);
 
   // Stage t -> slot t % kD. Load j of this wave fills 1 KiB block b = kLoads * wave + j of the stage: blocks 0-3 are
   // the 32 weight rows, the rest the code rows. Stages past K read zeros, so every stage issues the same loads.
@@ -99,8 +103,8 @@ __global__ __launch_bounds__(64 * kSfWaves, 1) void skinny_fused_kernel(
   for (int t = 0; t < nst; ++t) {
     // Every wave's share of stage t has landed; every wave is done with stage t - 1's slot, which stage t + kD - 1
     // refills.
-    static_assert(kWaitVm == 30, "the wait count below");
-    asm volatile("s_waitcnt vmcnt(30) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    static_assert(kWaitVm == 18, "the wait count below");
+    asm volatile("s_waitcnt vmcnt(18) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     issue(t + kD - 1);
     const unsigned char HF_LDS* stg = smem + (t % kD) * kStage;
 #pragma unroll
@@ -137,8 +141,8 @@ __global__ __launch_bounds__(64 * kSfWaves, 1) void skinny_fused_kernel(
       for (int wv = 0; wv < kSfWaves; ++wv) s += red[((wv * kJB + jb) * 16 + v) * 64 + lane];
       sums[v] = s;
     }
-    block_finish(ops[i], sums, 32 * jb, n0, u, ldu, up, ldup, r, bias, y, ldy, M, N, vec, act, glu_half,
-                 glu_gate_first, lane);
+    block_finish(ops[i], sums, 32 * jb, n0, u, ldu, up, ldup, r, bias, y, ldy, M, GLU ? N : n_end, vec, act,
+                 glu_half, glu_gate_first, lane);
   }
 }
 
@@ -146,7 +150,7 @@ __global__ __launch_bounds__(64 * kSfWaves, 1) void skinny_fused_kernel(
   template __global__ void skinny_fused_kernel<MR, GLU>(const int8_t*, int64_t, const int8_t*, int64_t,              \
                                                         const float*, const float*, const uint16_t*, int64_t,       \
                                                         const uint16_t*, int64_t, int, const uint16_t*, uint16_t*,  \
-                                                        int64_t, int, int, int, int, int, int, int);
+                                                        int64_t, int, int, int, int, int, int, int, int);
 HF_SF_INSTANTIATE(64, false) HF_SF_INSTANTIATE(64, true)
 #undef HF_SF_INSTANTIATE
 
