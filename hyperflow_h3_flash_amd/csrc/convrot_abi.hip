@@ -316,6 +316,9 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
     // Wide ranks with many rows: the persistent 256 x 256 tiles' bf16 product (x rows against down rows, K in
     // bytes), one pass over x per 256 ranks with the matrix cores at the tile kernel's rate. The summation order
     // (64-element stages, 16-element MFMA steps, K ascending) is lowrank_down_wide_kernel's.
+    if (2 * K >= (int64_t(1) << 31) || 2 * hf::GBM * ldx >= (int64_t(1) << 32) ||
+        2 * hf::GBN * ld_down >= (int64_t(1) << 32))
+      return HF_ERR_SIZE;
     hf::GemmArgs a{};
     a.q = reinterpret_cast<const int8_t*>(x); a.ldq = 2 * ldx;
     a.w = reinterpret_cast<const int8_t*>(down); a.ldw = 2 * ld_down;
@@ -325,8 +328,6 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
     a.tiles_n = (int)((r + hf::GBN - 1) / hf::GBN);
     a.splits = 1;
     a.k_chunk = (int)((a.K + hf::GBK - 1) / hf::GBK * hf::GBK);
-    if ((int64_t)hf::GBM * a.ldq >= (int64_t(1) << 32) || (int64_t)hf::GBN * a.ldw >= (int64_t(1) << 32))
-      return HF_ERR_SIZE;
     const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
     hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutMmBf16>, dim3((unsigned)gemm_grid(tiles)), dim3(hf::kThreads),
                        hf::kGemmLds, s, a);
