@@ -65,6 +65,9 @@ def parse_args():
     p.add_argument("--ceilings", action="store_true",
                    help="only measure the device's ceilings (INT8 MFMA with no memory traffic, a device copy's "
                         "bandwidth) and exit; the headline run reports them too")
+    p.add_argument("--operand-sweep", action="store_true",
+                   help="time the headline GEMM (same kernel, rank-64 epilogue) on operand sets of different bit "
+                        "toggling: the bench's codes and weights, all zero, all one, narrow codes, zero weights")
     p.add_argument("--vendor-gemm", action="store_true",
                    help="only time the vendor library's own INT8, FP8 and bf16 GEMMs at the headline shape (a "
                         "calibration of what the matrix cores sustain, not this build's path) and exit")
@@ -166,6 +169,60 @@ def ceilings(torch, repeats=5):
         result[name] = round(best, 1)
     del src, dst, sink
     return result
+
+
+def gemm_operand_sets(torch, dev, xq, qweight):
+    """Operand sets for the headline GEMM that differ only in how many operand bits toggle: the bench's own codes
+    (rotated activations) and weights, all zero, all one (constant bits), codes and weights uniform in [-20, 20],
+    and the bench's codes against zero weights. The GEMM's dataflow (loads, LDS traffic, MFMA count, epilogue and
+    stores) is the same for every set."""
+    gen = torch.Generator(device=dev).manual_seed(11)
+    return {
+        "bench": (xq, qweight),
+        "zero": (torch.zeros_like(xq), torch.zeros_like(qweight)),
+        "ones": (torch.ones_like(xq), torch.ones_like(qweight)),
+        "narrow": (torch.randint(-20, 21, xq.shape, device=dev, dtype=torch.int8, generator=gen),
+                   torch.randint(-20, 21, qweight.shape, device=dev, dtype=torch.int8, generator=gen)),
+        "zero_weights": (xq, torch.zeros_like(qweight)),
+    }
+
+
+def operand_sweep(torch, rounds=5, calls=4):
+    """The headline GEMM (M=32768, K=5120, N=15360, rank-64 epilogue) on each of gemm_operand_sets, interleaved
+    round by round after a warm-up, HIP events on the launch stream; one JSON line of median microseconds per call
+    and TOPS. Under `rocprofv3 --pmc` the launches come in a fixed order: 2 warm-up calls per set, then per round
+    `calls` calls of each set in the order of the dict."""
+    from hyperflow_h3_flash_amd.int8 import _kernels
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    kernels = _kernels()
+    x, qweight, wscale, down, up = make_inputs(torch, dev)
+    with torch.no_grad():
+        xq, sx = kernels.rotate_quant(x, GROUP)
+        u = kernels.lowrank_down(x, down)
+    del x
+    sets = gemm_operand_sets(torch, dev, xq, qweight)
+    stream = torch.cuda.current_stream(dev)
+    times = {name: [] for name in sets}
+    for q, w in sets.values():
+        for _ in range(2):
+            kernels.int8_matmul(q, w, sx, wscale, u=u, up=up)
+    torch.cuda.synchronize()
+    for _ in range(rounds):
+        for name, (q, w) in sets.items():
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(calls):
+                kernels.int8_matmul(q, w, sx, wscale, u=u, up=up)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times[name].append(e0.elapsed_time(e1) * 1e3 / calls)
+    ops = 2.0 * M * N * K
+    us = {name: round(statistics.median(v), 1) for name, v in times.items()}
+    print(json.dumps({"operand_sweep_us": us,
+                      "operand_sweep_TOPS": {name: round(ops / (t * 1e-6) / 1e12, 1) for name, t in us.items()},
+                      "config": {"M": M, "K": K, "N": N, "rank": RANK}}), flush=True)
 
 
 def make_inputs(torch, dev, seed=0):
@@ -307,6 +364,9 @@ def main():
     if args.copy_probe:
         copy_probe(torch)
         return
+    if args.operand_sweep:
+        operand_sweep(torch)
+        return
     if args.ceilings:
         print(json.dumps({"ceilings": ceilings(torch), "published": {"mfma_int8_TOPS": PEAK_INT8_TOPS,
                                                                       "hbm_GBs": PEAK_HBM_GBS}}), flush=True)
@@ -406,6 +466,24 @@ def main():
     # pass against a device copy's bandwidth (measured after the timed region).
     ceil = ceilings(torch)
     ceil["gemm_frac_of_mfma_uniform"] = round(gemm_tops / ceil["mfma_int8_uniform_TOPS"], 4)
+    # The same GEMM call (same kernel, dataflow and epilogue) with all-zero codes and weights: the rate of this
+    # dataflow when the operand bits do not toggle, i.e. with the power the random operands draw taken away.
+    with torch.no_grad():
+        xq0, sx0 = kernels.rotate_quant(x, GROUP)
+        u0 = kernels.lowrank_down(x, layer.down.weight)
+        xq0.zero_()
+        w0 = torch.zeros_like(layer.qweight)
+        for _ in range(2):
+            kernels.int8_matmul(xq0, w0, sx0, layer.wscale, u=u0, up=layer.up.weight)
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        e[0].record(stream)
+        for _ in range(5):
+            kernels.int8_matmul(xq0, w0, sx0, layer.wscale, u=u0, up=layer.up.weight)
+        e[1].record(stream)
+        torch.cuda.synchronize()
+        ceil["gemm_zero_operands_TOPS"] = round(ops / (e[0].elapsed_time(e[1]) * 1e-3 / 5) / 1e12, 1)
+        del xq0, sx0, u0, w0
+    ceil["gemm_frac_of_zero_operands"] = round(gemm_tops / ceil["gemm_zero_operands_TOPS"], 4)
     ceil["rotate_quant_frac_of_copy"] = round(result["rotate_quant_GBs"] / ceil["copy_GBs"], 4)
     ceil["rotate_quant_frac_of_stream"] = round(result["rotate_quant_GBs"] / ceil["stream_r2w1_GBs"], 4)
     ceil["lowrank_down_frac_of_stream"] = round(result["lowrank_down_GBs"] / ceil["stream_read_GBs"], 4)

@@ -58,6 +58,13 @@ void allow_large_lds() {
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActSwiGLU>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+#define HF_LATE_ATTR(OUT, ACT)                                                                                       \
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::int8_gemm_kernel<OUT, ACT, true>),                 \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::kGemmLds);
+    HF_LATE_ATTR(hf::kOutBf16, hf::kActNone) HF_LATE_ATTR(hf::kOutBf16Lr, hf::kActNone)
+    HF_LATE_ATTR(hf::kOutBf16, hf::kActGeluTanh) HF_LATE_ATTR(hf::kOutBf16Lr, hf::kActGeluTanh)
+    HF_LATE_ATTR(hf::kOutBf16, hf::kActSwiGLU) HF_LATE_ATTR(hf::kOutBf16Lr, hf::kActSwiGLU)
+#undef HF_LATE_ATTR
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_fused_kernel<64, false>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, hf::sf_lds(64));
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_fused_kernel<64, true>),
@@ -219,20 +226,23 @@ int launch_gemm(hf::GemmArgs& a, bool i32, hipStream_t stream, int act = hf::kAc
       hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutI32, hf::kActSwiGLU>), grid, block, hf::kGemmLds, stream, a);
     else
       hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutI32>, grid, block, hf::kGemmLds, stream, a);
-  } else if (a.r > 0 && a.r <= 64) {
-    if (act == hf::kActGeluTanh)
-      hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActGeluTanh>), grid, block, hf::kGemmLds, stream, a);
-    else if (act == hf::kActSwiGLU)
-      hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16Lr, hf::kActSwiGLU>), grid, block, hf::kGemmLds, stream, a);
-    else
-      hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16Lr>, grid, block, hf::kGemmLds, stream, a);
   } else {
-    if (act == hf::kActGeluTanh)
-      hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16, hf::kActGeluTanh>), grid, block, hf::kGemmLds, stream, a);
-    else if (act == hf::kActSwiGLU)
-      hipLaunchKernelGGL((hf::int8_gemm_kernel<hf::kOutBf16, hf::kActSwiGLU>), grid, block, hf::kGemmLds, stream, a);
-    else
-      hipLaunchKernelGGL(hf::int8_gemm_kernel<hf::kOutBf16>, grid, block, hf::kGemmLds, stream, a);
+    // Stage loads after each K step's MFMAs up to K = kLateLoadsMaxK (int8_gemm_kernel's LATE, measured by K).
+    const bool late = a.splits == 1 && a.K <= hf::kLateLoadsMaxK;
+    const bool lr = a.r > 0 && a.r <= 64;
+#define HF_GEMM_BF16(OUT, ACT)                                                                                      \
+    if (late)                                                                                                       \
+      hipLaunchKernelGGL((hf::int8_gemm_kernel<OUT, ACT, true>), grid, block, hf::kGemmLds, stream, a);             \
+    else                                                                                                            \
+      hipLaunchKernelGGL((hf::int8_gemm_kernel<OUT, ACT, false>), grid, block, hf::kGemmLds, stream, a);
+    if (act == hf::kActGeluTanh) {
+      if (lr) { HF_GEMM_BF16(hf::kOutBf16Lr, hf::kActGeluTanh) } else { HF_GEMM_BF16(hf::kOutBf16, hf::kActGeluTanh) }
+    } else if (act == hf::kActSwiGLU) {
+      if (lr) { HF_GEMM_BF16(hf::kOutBf16Lr, hf::kActSwiGLU) } else { HF_GEMM_BF16(hf::kOutBf16, hf::kActSwiGLU) }
+    } else {
+      if (lr) { HF_GEMM_BF16(hf::kOutBf16Lr, hf::kActNone) } else { HF_GEMM_BF16(hf::kOutBf16, hf::kActNone) }
+    }
+#undef HF_GEMM_BF16
   }
   return launch_status();
 }

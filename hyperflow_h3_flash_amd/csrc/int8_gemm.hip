@@ -17,7 +17,7 @@
 // Operands: K is consumed in stages of 128 bytes. A stage (256 rows of q and 256 rows of w, 128 bytes each: 64 KiB)
 // goes global -> LDS with buffer_load ... lds, 16 bytes per lane, 8 lanes per row, so every load instruction moves
 // 8 whole 128-byte lines (half-line requests measured 11 % slower: the texture-address FIFOs fill). Two stage slots
-// alternate (double buffering): the loads of stage s + 2 are issued, two at a time between MFMAs, while stage s + 1
+// alternate (double buffering): the loads of stage s + 2 are issued after the MFMAs of a K step, while stage s + 1
 // is multiplied. Waits are exact vmcnt counts; the barrier carries no memory fence. MFMA operands are
 // double-buffered in registers (the LDS reads of one 32-byte K step overlap the MFMAs of the previous one).
 // Out-of-range rows and K beyond the end read as zero through the buffer descriptor's range check.
@@ -265,11 +265,14 @@ __device__ __forceinline__ void wait_vm(int n) {
 // product: q and w hold bf16 rows (ldq, ldw and K in bytes), the sums are fp32 and the output is bf16(sum + bias)
 // (the low-rank up projection, whose small K and large output suit the persistent tiles and their whole-line stores).
 constexpr int kOutI32 = 0, kOutBf16 = 1, kOutBf16Lr = 2, kOutMmBf16 = 3;
+// Deepest K for which the bf16-output GEMMs issue their stage loads after a K step's MFMAs (LATE).
+constexpr int kLateLoadsMaxK = 8192;
 
 
 // Persistent kernel: one workgroup per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... Every wave issues the
-// same number of memory operations in the same order, so every wait is a constant vmcnt.
-template <int OUT, int ACT = kActNone>
+// same number of memory operations in the same order, so every wait is a constant vmcnt. LATE places each stage's
+// loads after the MFMAs of the K step that issues them instead of two per MFMA among them (the host's choice by K).
+template <int OUT, int ACT = kActNone, bool LATE = false>
 __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char smem_raw[];
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)smem_raw;
@@ -314,7 +317,11 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
   v16i acc[NB][4];
 
   // MFMAs of one K step on `use` with the LDS reads of the next fragments (`read`) spread between them, two per
-  // MFMA, and, when `loads` issues a stage's loads, those two per MFMA after them.
+  // MFMA, and, when `loads` issues a stage's loads, those two per MFMA after them or (LATE) after the step's last
+  // MFMA. Every wave issues its share of a stage right after the barrier; issued late, a load whose issue waits for
+  // the texture unit holds up no MFMA of the step. Measured (GEMM with the rank-64 epilogue, same box, bitwise
+  // equal): late 0.7-1.1 % faster at K = 5120-7168 (M=32768, N=15360: 2135 -> 2112 us; M=37710, K=5376, N=7168:
+  // 1257 -> 1240 us), but 2.7-4.4 % slower at K = 13824-14336 (M=37710, K=14336, N=5376: 2486 -> 2583 us).
   auto kstep = [&](const Frags& use, auto&& read, auto&& loads) {
     read();
     mma<OUT == kOutMmBf16>(acc, use);
@@ -324,12 +331,17 @@ __global__ __launch_bounds__(kThreads, 1) void int8_gemm_kernel(GemmArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
     }
+    if constexpr (LATE) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * NB, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, kStageLoads, 0);  // VMEM (stage loads)
+    } else {
 #pragma unroll
-    for (int i = 0; i < kStageLoads / 2; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM (stage loads)
+      for (int i = 0; i < kStageLoads / 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM (stage loads)
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * NB, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4 * NB, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
   auto nothing = [] {};
@@ -749,5 +761,12 @@ template __global__ void int8_gemm_kernel<kOutBf16Lr, kActGeluTanh>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16, kActSwiGLU>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutBf16Lr, kActSwiGLU>(GemmArgs);
 template __global__ void int8_gemm_kernel<kOutMmBf16>(GemmArgs);  // bf16 product (the low-rank up projection)
+// Late stage loads (whole-K bf16-output GEMMs with K <= kLateLoadsMaxK).
+template __global__ void int8_gemm_kernel<kOutBf16, kActNone, true>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16Lr, kActNone, true>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16, kActGeluTanh, true>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16Lr, kActGeluTanh, true>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16, kActSwiGLU, true>(GemmArgs);
+template __global__ void int8_gemm_kernel<kOutBf16Lr, kActSwiGLU, true>(GemmArgs);
 
 }  // namespace hf
