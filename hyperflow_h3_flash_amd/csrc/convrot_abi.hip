@@ -119,6 +119,13 @@ void allow_large_lds() {
                               hipFuncAttributeMaxDynamicSharedMemorySize, hf::kMidLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::mid_gemm_kernel<hf::kActGeluTanh>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, hf::kMidLds);
+#define HF_BAND_ATTR(NB)                                                                                            \
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::band_gemm_kernel<NB, hf::kActNone>),              \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::band_lds(NB));                       \
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::band_gemm_kernel<NB, hf::kActGeluTanh>),          \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::band_lds(NB));
+    HF_BAND_ATTR(3) HF_BAND_ATTR(4) HF_BAND_ATTR(5)
+#undef HF_BAND_ATTR
 #define HF_SKINNY_ATTR(GLU, MR)                                                                       \
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::skinny_gemm_kernel<GLU, MR>),             \
                               hipFuncAttributeMaxDynamicSharedMemorySize, hf::skinny_lds(MR));
@@ -517,6 +524,22 @@ bool use_mid_gemm(int64_t M, int64_t N, int64_t K, int32_t r, bool glu) {
   return t_round < t_split;
 }
 
+// Column blocks per 128-row band tile (band_gemm_kernel), or 0: the bands run when one round of them fills at least
+// 7/8 of the CUs while the 256 x 128 tiles would fill at most 3/4 (M=1024: N=5120 as 256 tiles of 128 x 160
+// against 160 of 256 x 128; N=4096, 128 x 128; N=3072, 128 x 96). The widest such tile wins: it reads the fewest
+// operand bytes per output. Rank <= 64, no SwiGLU.
+int band_blocks_n(int64_t M, int64_t N, int32_t r, bool glu) {
+  if (glu || r > 64) return 0;
+  const int64_t cus = device_cus();
+  const int64_t mid_tiles = ((M + hf::kMidBM - 1) / hf::kMidBM) * ((N + hf::kMidBN - 1) / hf::kMidBN);
+  if (4 * mid_tiles > 3 * cus && mid_tiles <= cus) return 0;
+  for (int nb = 5; nb >= 3; --nb) {
+    const int64_t tiles = ((M + hf::kBandBM - 1) / hf::kBandBM) * ((N + 32 * nb - 1) / (32 * nb));
+    if (tiles <= cus && 8 * tiles >= 7 * cus) return nb;
+  }
+  return 0;
+}
+
 // Whether a GEMM of at most 64 rows runs in one pass (skinny_fused_kernel): its 32-row weight slices fill between a
 // quarter of the CUs and one round of them. Each workgroup's weight stream is latency-bound (the codes take two thirds
 // of each stage), so against the split-K path (128-row slices over K chunks, partial planes and a finishing pass) it
@@ -560,7 +583,7 @@ int64_t partial_plane_ints(int64_t M, int64_t N) { return ((M + 31) / 32) * ((N 
 // size queries report its bytes, so a query gives exactly what the call with the same sizes, rank and activation
 // uses (0 for the 256 x 128 tiles, the one-pass few-row kernel and whole tiles).
 struct GemmRoute {
-  enum Kind { kWhole, kPeel, kMid, kSkinnyFused, kSplit } kind = kWhole;
+  enum Kind { kWhole, kPeel, kBand, kMid, kSkinnyFused, kSplit } kind = kWhole;
   int64_t m_main = 0;    // kPeel: rows run as whole tiles; the rest run by their own route
   GemmPlan plan;         // kSplit: the K split
   int64_t ws_bytes = 0;  // workspace the route uses (kPeel: the peeled rows' route's)
@@ -573,6 +596,10 @@ GemmRoute gemm_route(int64_t M, int64_t N, int64_t K, int32_t r, bool glu) {
     route.kind = GemmRoute::kPeel;
     route.m_main = m_main;
     route.ws_bytes = gemm_route(M - m_main, N, K, r, glu).ws_bytes;
+    return route;
+  }
+  if (band_blocks_n(M, N, r, glu)) {
+    route.kind = GemmRoute::kBand;
     return route;
   }
   if (use_mid_gemm(M, N, K, r, glu)) {
@@ -646,6 +673,26 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
     if (st != HF_OK) return st;
     return int8_linear_impl(q, ldq, w, ldw, sx, sw, u, ldu, up, ld_up, r, bias, y, ldy, m_main, N, K, nullptr, 0,
                             stream, act_code);
+  }
+  if (route.kind == GemmRoute::kBand) {
+    allow_large_lds();
+    const int nb = band_blocks_n(M, N, r, glu);
+    hf::MidArgs a{};
+    a.q = q; a.ldq = ldq; a.w = w; a.ldw = ldw; a.sx = sx; a.sw = sw;
+    a.u = r > 0 ? u : nullptr; a.ldu = ldu; a.up = r > 0 ? up : nullptr; a.ldup = ld_up; a.r = r;
+    a.bias = bias; a.y = y; a.ldy = ldy; a.M = (int)M; a.N = (int)N; a.K = (int)K;
+    a.tiles_m = (int)((M + hf::kBandBM - 1) / hf::kBandBM);
+    a.tiles_n = (int)((N + 32 * nb - 1) / (32 * nb));
+    a.out_vec16 = aligned(y, 16) && (ldy % 8) == 0;
+    const dim3 grid((unsigned)((int64_t)a.tiles_m * a.tiles_n)), block(hf::kBandThreads);
+#define HF_BAND_LAUNCH(NB)                                                                                          \
+    if (act == hf::kActGeluTanh)                                                                                    \
+      hipLaunchKernelGGL((hf::band_gemm_kernel<NB, hf::kActGeluTanh>), grid, block, hf::band_lds(NB), s, a);        \
+    else                                                                                                            \
+      hipLaunchKernelGGL((hf::band_gemm_kernel<NB, hf::kActNone>), grid, block, hf::band_lds(NB), s, a);
+    if (nb == 5) { HF_BAND_LAUNCH(5) } else if (nb == 4) { HF_BAND_LAUNCH(4) } else { HF_BAND_LAUNCH(3) }
+#undef HF_BAND_LAUNCH
+    return launch_status();
   }
   if (route.kind == GemmRoute::kMid) {
     allow_large_lds();

@@ -115,12 +115,13 @@ def test_split_planner_follows_the_measured_cost_models(lib):
 
 def test_workspace_queries_report_what_the_route_uses(lib):
     """The size queries follow the kernel route the call takes: no workspace for the one-pass few-row kernel
-    (M <= 64 with 32-row weight slices on a quarter to one round of CUs) or for the 256 x 128 tiles (config 1's
-    layer), the split plan's partial planes otherwise; the 256 x 128 tiles cover rank <= 64 without SwiGLU, so the
-    same sizes with rank 96 or SwiGLU take the split path and report its planes."""
+    (M <= 64 with 32-row weight slices on a quarter to one round of CUs), for the 128-row band tiles (config 1's
+    layer) or for the 256 x 128 tiles, the split plan's partial planes otherwise; both tile kernels cover rank <= 64
+    without SwiGLU, so the same sizes with rank 96 or SwiGLU take the split path and report its planes."""
     assert lib.hf_int8_linear_ws_bytes(64, 5120, 5120, 32, 0) == 0  # one pass
     assert lib.hf_int8_linear_ws_bytes(17, 2048, 4096, 16, 1) == 0  # one pass, tanh-GELU
-    assert lib.hf_int8_linear_ws_bytes(1024, 3072, 3072, 32, 0) == 0  # 256 x 128 tiles
+    assert lib.hf_int8_linear_ws_bytes(1024, 3072, 3072, 32, 0) == 0  # 128 x 96 band tiles
+    assert lib.hf_int8_linear_ws_bytes(1024, 5120, 5120, 64, 1) == 0  # 128 x 160 band tiles, tanh-GELU
     assert lib.hf_int8_linear_ws_bytes(1024, 3072, 3072, 96, 0) > 0
     assert lib.hf_int8_linear_ws_bytes(1024, 3072, 3072, 32, 2) > 0  # SwiGLU
     assert lib.hf_int8_linear_ws_bytes(256, 30720, 5120, 32, 0) == 0  # 256 x 128 tiles

@@ -36,9 +36,22 @@ def bits_of(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def takes_mid_path(m: int, n: int) -> bool:
-    """The host's rule (use_mid_gemm) on this device."""
+def takes_band_path(m: int, n: int, r: int) -> bool:
+    """The host's rule for the 128-row band tiles (band_blocks_n) on this device: one round of them fills at least
+    7/8 of the CUs while the 256 x 128 tiles would fill at most 3/4."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
+    mid_tiles = -(-m // 256) * -(-n // 128)
+    if r > 64 or (4 * mid_tiles > 3 * cus and mid_tiles <= cus):
+        return False
+    return any(cus >= -(-m // 128) * -(-n // (32 * nb)) and 8 * -(-m // 128) * -(-n // (32 * nb)) >= 7 * cus
+               for nb in (5, 4, 3))
+
+
+def takes_mid_path(m: int, n: int, r: int = 0) -> bool:
+    """The host's rule (use_mid_gemm, after the band tiles' rule) on this device."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if takes_band_path(m, n, r):
+        return False
     tiles_m = -(-m // 256)
     if tiles_m * -(-n // 256) >= cus:
         return False
@@ -49,11 +62,11 @@ def takes_mid_path(m: int, n: int) -> bool:
 
 CASES = [
     # m, k, n, group, rank, bias
-    (1024, 5120, 5120, 256, 0, False),
-    (1024, 5120, 5120, 256, 32, False),
+    (1024, 5120, 7168, 256, 0, False),
+    (1024, 5120, 7168, 256, 32, False),
     (256, 5120, 30720, 256, 32, False),
-    (700, 5136, 6000, 16, 0, False),
-    (700, 5136, 6000, 16, 24, True),
+    (700, 5136, 8000, 16, 0, False),
+    (700, 5136, 8000, 16, 24, True),
     (300, 256, 16384, 256, 0, False),
     (300, 256, 16384, 256, 64, True),
     (520, 384, 8192, 64, 16, False),
@@ -89,7 +102,7 @@ def sampled(m, seed, count=16):
 
 @pytest.mark.parametrize("m,k,n,g,r,bias", CASES)
 def test_mid_tiles_match_the_oracle(oracle_lib, m, k, n, g, r, bias):
-    assert takes_mid_path(m, n), "this shape should take the 256 x 128 tile kernel"
+    assert takes_mid_path(m, n, r), "this shape should take the 256 x 128 tile kernel"
     x, layer = layer_for(m, k, n, g, r, bias, seed=m + n + r)
     with torch.no_grad():
         y = layer(x)
@@ -120,9 +133,9 @@ def test_mid_tiles_match_the_oracle(oracle_lib, m, k, n, g, r, bias):
     assert np.abs(g32 - comp).max() / np.abs(comp).max() <= 1e-2
 
 
-@pytest.mark.parametrize("m,k,n,r", [(1024, 5120, 5120, 64), (700, 2048, 6000, 0)])
+@pytest.mark.parametrize("m,k,n,r", [(1024, 5120, 7168, 64), (700, 2048, 8000, 0)])
 def test_mid_tiles_gelu_epilogue(oracle_lib, m, k, n, r):
-    assert takes_mid_path(m, n)
+    assert takes_mid_path(m, n, r)
     x, layer = layer_for(m, k, n, 256, r, False, seed=7 + m, activation="gelu_tanh")
     with torch.no_grad():
         h = layer(x)
@@ -141,9 +154,10 @@ def test_mid_tiles_gelu_epilogue(oracle_lib, m, k, n, r):
 def test_mid_tiles_agree_with_the_persistent_tiles_bitwise():
     """The same layer (with a bias) through the 256 x 128 tiles and, as part of a 4096-row batch, through the
     persistent 256 x 256 tiles: rows are computed independently by the same arithmetic, so they agree bit for bit."""
-    x, layer = layer_for(1024, 5120, 5120, 256, 0, True, seed=3)
+    x, layer = layer_for(1024, 5120, 7168, 256, 0, True, seed=3)
+    assert takes_mid_path(1024, 7168)
     big = torch.cat([x, x, x, x], dim=0)  # 4096 rows: 256 x 256 tiles fill the CUs, no mid path
-    assert not takes_mid_path(4096, 5120)
+    assert not takes_mid_path(4096, 7168)
     with torch.no_grad():
         y_mid = layer(x)
         y_big = layer(big)

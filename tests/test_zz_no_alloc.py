@@ -67,12 +67,12 @@ def run(lib, c, noalloc: bool, act: int = 0):
 
 
 # (m, k, n, rank, bias, activation), every call using the scratch: the split low-rank down projection ahead of the
-# 256 x 128 tiles, then the skinny kernel's K split; the skinny K split at 256 and at 64 rows (too many weight slices
+# 128-row band tiles, then the skinny kernel's K split; the skinny K split at 128 and at 64 rows (too many weight slices
 # for the one-pass kernel); SwiGLU in pair order, then tanh-GELU, both split over K. Each pair runs the larger input
 # first.
 PAIRS = [
     ((1024, 5120, 5120, 32, True, 0), (300, 3072, 3072, 64, False, 0)),
-    ((256, 5120, 15360, 32, False, 0), (64, 5120, 30720, 32, True, 0)),
+    ((128, 5120, 30720, 32, False, 0), (64, 5120, 30720, 32, True, 0)),
     ((200, 5376, 14336, 64, True, 2), (17, 2048, 16384, 16, False, 1)),
 ]
 
