@@ -119,6 +119,8 @@ void allow_large_lds() {
                               hipFuncAttributeMaxDynamicSharedMemorySize, hf::kMidLds);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::mid_gemm_kernel<hf::kActGeluTanh>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, hf::kMidLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::lowrank_down_band_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, hf::kLbLds);
 #define HF_BAND_ATTR(NB)                                                                                            \
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&hf::band_gemm_kernel<NB, hf::kActNone>),              \
                               hipFuncAttributeMaxDynamicSharedMemorySize, hf::band_lds(NB));                       \
@@ -327,6 +329,23 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
                           !aligned(ws, 16))) {
     plan = LrPlan{};  // no (or too small a) workspace: one pass over K
     plan.k_chunk = (int)K;
+  }
+  if (plan.splits == 1 && r > 128 && K >= 4096 && 8 * ((M + hf::kLbRows - 1) / hf::kLbRows) >= 7 * device_cus() &&
+      8 * ((M + hf::kLbRows - 1) / hf::kLbRows) <= 8 * device_cus()) {
+    // Ranks past 128 with 160-row blocks filling 7/8 to all of the CUs: lowrank_down_band_kernel, 256 ranks per pass
+    // over x, bitwise the sums of the routes below. Measured at M=37710 against them (same box): K=14336, r=256 387
+    // -> 333 us, r=512 731 -> 657 us; K=5376, r=192 149 -> 120 us, r=256 155 -> 147 us, r=512 259 -> 256 us. With a
+    // short K (M=40000, K=2064, r=200: 59 -> 80 us) the four-stage x ring does not fill, hence K >= 4096.
+    if (2 * hf::kLwRanks * ld_down >= (int64_t(1) << 31)) return HF_ERR_SIZE;
+    const unsigned blocks = (unsigned)((M + hf::kLbRows - 1) / hf::kLbRows);
+    for (int32_t j0 = 0; j0 < r; j0 += hf::kLwRanks) {
+      const int rr = std::min<int32_t>(hf::kLwRanks, r - j0);
+      hipLaunchKernelGGL(hf::lowrank_down_band_kernel, dim3(blocks), dim3(512), hf::kLbLds, s, x, ldx,
+                         down + (int64_t)j0 * ld_down, ld_down, u + j0, ldu, (int)M, (int)K, rr);
+      const int st = launch_status();
+      if (st != HF_OK) return st;
+    }
+    return HF_OK;
   }
   if (plan.splits == 1 && r >= 192 && aligned(u, 16) && (ldu % 8) == 0 &&
       2 * ((M + hf::GBM - 1) / hf::GBM) * ((r + hf::GBN - 1) / hf::GBN) >= device_cus()) {

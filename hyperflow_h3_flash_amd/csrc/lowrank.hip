@@ -266,6 +266,126 @@ template __global__ void lowrank_down_wide_kernel<4>(const uint16_t*, int64_t, c
 template __global__ void lowrank_down_wide_kernel<5>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
                                                      int64_t, int, int, int);
 
+// lowrank_down_wide_kernel's tile (160 rows of x against 256 ranks per pass) on 8 waves instead of 10, with x and
+// down in rings of their own. Wave w multiplies all five 32-row blocks against ranks 32 w .. 32 w + 31 (five MFMA
+// blocks, one down fragment and five x fragments per K step), so every SIMD holds two waves; with ten, two SIMDs held
+// three and set the pace. x streams from HBM and its rate follows the bytes in flight (a 52 KiB stage of which the
+// 256-rank down slab takes 32 KiB left one stage of x in flight: ~2.8 TB/s), so x gets a 4-slot ring (three stages
+// ahead) loaded by waves 0-3 and down, read from L2, a 2-slot ring (one stage ahead) loaded by waves 4-7: each
+// wave's in-order vmcnt wait covers only its own ring. The fragments of the next K step are read while the current
+// one's MFMAs run. Each u element is the same sum in the same order as lowrank_down_wide_kernel's (and the 64-rank
+// passes'): K ascending in 16-element MFMA steps, down as the first operand.
+constexpr int kLbRows = 160;
+constexpr int kLbXBytes = kLbRows * kLrStageK * 2;   // 20 KiB a stage of x
+constexpr int kLbDBytes = kLwRanks * kLrStageK * 2;  // 32 KiB a stage of down
+constexpr int kLbXSlots = 4, kLbDSlots = 2;
+constexpr int kLbLds = kLbXSlots * kLbXBytes + kLbDSlots * kLbDBytes;  // 144 KiB
+constexpr int kLbXLoads = kLbRows / 8 / 4;   // 5 per x wave and stage
+constexpr int kLbDLoads = kLwRanks / 8 / 4;  // 8 per down wave and stage
+
+__global__ __launch_bounds__(512, 1) void lowrank_down_band_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                   const uint16_t* __restrict__ down, int64_t ldd,
+                                                                   uint16_t* __restrict__ u, int64_t ldu, int M, int K,
+                                                                   int r) {
+  static_assert(kLbLds <= 160 * 1024, "rings exceed the LDS");
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lb_smem_raw[];
+  unsigned char HF_LDS* smem = (unsigned char HF_LDS*)lb_smem_raw;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane & 31, half = lane >> 5;
+  const bool xw = wave < 4;  // x loader (waves 0-3) or down loader (waves 4-7)
+  const int m0 = blockIdx.x * kLbRows;
+  const int rows_m = min(kLbRows, M - m0);
+  const uint32_t ldx_bytes = (uint32_t)ldx * 2u, ldd_bytes = (uint32_t)ldd * 2u;
+  const uint32_t bytes_x = (uint32_t)rows_m * ldx_bytes, bytes_d = (uint32_t)r * ldd_bytes;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + (int64_t)m0 * ldx, bytes_x);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(down, bytes_d);
+  auto xslot = [&](int t) { return smem + (t % kLbXSlots) * kLbXBytes; };
+  auto dslot = [&](int t) { return smem + kLbXSlots * kLbXBytes + (t % kLbDSlots) * kLbDBytes; };
+  // This wave's loads of stage t: x blocks 5 w .. 5 w + 4, or down blocks 8 (w - 4) .. 8 (w - 4) + 7 (8 rows each;
+  // stages past the end read zeros).
+  auto issue_x = [&](int t) {
+    lr_load<kLbXLoads, kCpolStream>(rx, bytes_x, ldx_bytes, rows_m, t * kLrStageK, K, xslot(t), wave * kLbXLoads, lane);
+  };
+  auto issue_d = [&](int t) {
+    lr_load<kLbDLoads>(rd, bytes_d, ldd_bytes, r, t * kLrStageK, K, dslot(t), (wave - 4) * kLbDLoads, lane);
+  };
+
+  v16f acc[5];
+#pragma unroll
+  for (int rb = 0; rb < 5; ++rb) acc[rb] = (v16f){0};
+  const bool live = wave * 32 < r;  // a wave whose ranks are all past r only loads
+  const int nst = (K + kLrStageK - 1) / kLrStageK;
+  if (xw) {
+#pragma unroll
+    for (int t = 0; t < kLbXSlots - 1; ++t) issue_x(t);
+  } else {
+    issue_d(0);
+  }
+  const int drow = wave * 32 + sub;
+  struct Frags {
+    v8bf d;
+    v8bf x[5];
+  };
+  auto read = [&](Frags& f, const unsigned char HF_LDS* xs, const unsigned char HF_LDS* ds, int s) {
+    const int c = 2 * s + half;
+    f.d = *reinterpret_cast<const v8bf HF_LDS*>(ds + drow * 128 + lr_swizzle(drow, c) * 16);
+#pragma unroll
+    for (int rb = 0; rb < 5; ++rb) {
+      const int xrow = rb * 32 + sub;
+      f.x[rb] = *reinterpret_cast<const v8bf HF_LDS*>(xs + xrow * 128 + lr_swizzle(xrow, c) * 16);
+    }
+  };
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int rb = 0; rb < 5; ++rb) acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.d, f.x[rb], acc[rb], 0, 0, 0);
+  };
+  Frags f0, f1;
+  for (int t = 0; t < nst; ++t) {
+    // Stage t has landed for this wave's ring (x waves: stages t + 1 and t + 2 still in flight; down waves: nothing)
+    // and its reads of stage t - 1 have returned; the barrier makes that true for every wave, so the slots of stage
+    // t - 1 take x stage t + 3 and down stage t + 1.
+    if (xw)
+      asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (xw)
+      issue_x(t + kLbXSlots - 1);
+    else
+      issue_d(t + 1);
+    if (!live) continue;
+    const unsigned char HF_LDS* xs = xslot(t);
+    const unsigned char HF_LDS* ds = dslot(t);
+    read(f0, xs, ds, 0);
+    read(f1, xs, ds, 1);
+    mma(f0);
+    read(f0, xs, ds, 2);
+    mma(f1);
+    read(f1, xs, ds, 3);
+    mma(f0);
+    mma(f1);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // zero-fill loads past the end may still be landing
+  if (!live) return;
+#pragma unroll
+  for (int rb = 0; rb < 5; ++rb) {
+    const int row = m0 + rb * 32 + sub;
+    if (row >= M) continue;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int j = wave * 32 + 8 * g + 4 * half;
+      uint16_t* dst = u + (int64_t)row * ldu + j;
+      if (j + 3 < r && (ldu & 3) == 0) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(acc[rb][4 * g], acc[rb][4 * g + 1]),
+                                                    pack_bf16x2(acc[rb][4 * g + 2], acc[rb][4 * g + 3]));
+      } else {
+        for (int e = 0; e < 4; ++e)
+          if (j + e < r) dst[e] = (uint16_t)f32_to_bf16_rne(acc[rb][4 * g + e]);
+      }
+    }
+  }
+}
+
 constexpr int kMaxSplits = 32;  // K chunks of a split launch, at most
 
 // u[m, j] = bf16(sum_s part[s][m][j]): the planes added in a fixed order, one rounding (round to nearest even).
