@@ -364,6 +364,22 @@ __global__ __launch_bounds__(512, 1) void lowrank_down_band_kernel(const uint16_
     read(f1, xs, ds, 3);
     mma(f0);
     mma(f1);
+    // Keep that order: left to itself the compiler moves each fragment read down to its MFMA, which then waits for
+    // it (lgkmcnt(0) before most MFMAs; 8-11 % slower). K steps 0 and 1 are read up front, K steps 2 and 3 among
+    // the MFMAs of the two steps before them.
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // DS read
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int i = 1; i < 5; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // zero-fill loads past the end may still be landing
   if (!live) return;
