@@ -115,18 +115,27 @@ __global__ __launch_bounds__(64 * NW, 1) void lowrank_down_kernel(const uint16_t
     }
     issue(t + kStages - 1);
     const unsigned char HF_LDS* st = smem + (t % kStages) * kStageBytes;
+    // All of the stage's fragments are read before its MFMAs (with one wave per SIMD nothing else hides a read the
+    // compiler would otherwise place right before its MFMA): 0-1.6 % faster, the same sums in the same order.
+    v8bf xf[kLrStageK / 16], df[kLrStageK / 16][RB];
 #pragma unroll
     for (int s = 0; s < kLrStageK / 16; ++s) {
       const int c = 2 * s + half;
-      const v8bf xf = *reinterpret_cast<const v8bf HF_LDS*>(st + xrow * 128 + lr_swizzle(xrow, c) * 16);
+      xf[s] = *reinterpret_cast<const v8bf HF_LDS*>(st + xrow * 128 + lr_swizzle(xrow, c) * 16);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         const int drow = rb * 32 + sub;
-        const v8bf df =
-            *reinterpret_cast<const v8bf HF_LDS*>(st + kXBytes + drow * 128 + lr_swizzle(drow, c) * 16);
-        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(df, xf, acc[rb], 0, 0, 0);
+        df[s][rb] = *reinterpret_cast<const v8bf HF_LDS*>(st + kXBytes + drow * 128 + lr_swizzle(drow, c) * 16);
       }
     }
+#pragma unroll
+    for (int s = 0; s < kLrStageK / 16; ++s)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(df[s][rb], xf[s], acc[rb], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, (kLrStageK / 16) * (1 + RB), 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, (kLrStageK / 16) * RB, 0);        // MFMA
+    __builtin_amdgcn_sched_barrier(0);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // zero-fill loads past the end may still be landing
 
