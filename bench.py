@@ -59,7 +59,8 @@ def parse_args():
     p.add_argument("--cpu-rows", type=int, default=32768, help="row sample for the CPU baseline")
     p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6, 7, 8),
                    help="workload: 2 (default) is the headline QKV projection; 1, 3-7 are supporting measurements")
-    p.add_argument("--rows", type=int, default=None, help="--config 5: only this M (64, 256 or 1024)")
+    p.add_argument("--rows", type=int, default=None,
+                   help="--config 5: only this M (64, 256 or 1024); --config 4: this many tokens (default 41344)")
     p.add_argument("--copy-probe", action="store_true",
                    help="only copy a 1 GiB device buffer 3 times (calibrates the HBM byte counters) and exit")
     p.add_argument("--ceilings", action="store_true",
@@ -563,7 +564,9 @@ def run_config(torch, config, steps, warmup, rows=None, cpu_rows=2048):
         elif config == 6:
             m, shapes, name = 32768, [(5376, 28672), (14336, 5376)], "gated FFN up + SwiGLU + down"
         else:
-            m = 41344
+            # The 5.2 s clip's block (40320 video + 1024 audio tokens); --rows gives one rank's share of it, e.g.
+            # 5168 rows for an 8-way split of the tokens.
+            m = rows or 41344
             shapes, name = [(5120, 15360), (5120, 5120), (5120, 13824), (13824, 5120)], "DiT block linears"
         built = [layer_inputs(torch, dev, m, k, n, 64, False, 0.005, 30.0, seed=3 + i) for i, (k, n) in
                  enumerate(shapes)]

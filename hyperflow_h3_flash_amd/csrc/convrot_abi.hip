@@ -155,15 +155,16 @@ int launch_rotate_wide(bool f32_recip, int lg, const uint16_t* x, int64_t ldx, i
 
 // rotate_quant_reg_kernel<lg, tpw, f32> (lg and tpw already range-checked by the caller).
 int launch_rotate_reg(int lg, int tpw, bool f32, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-                      const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int K, int wpr) {
+                      const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int K, int wpr,
+                      const hf::LrFinish& fin) {
 #define HF_RQ_CASE(L, T)                                                                                          \
   if (lg == L && tpw == T) {                                                                                      \
     if (f32)                                                                                                      \
       hipLaunchKernelGGL((hf::rotate_quant_reg_kernel<L, T, true>), grid, block, lds, s, x, ldx, q, ldq, sx, M, K, \
-                         wpr);                                                                                    \
+                         wpr, fin);                                                                               \
     else                                                                                                          \
       hipLaunchKernelGGL((hf::rotate_quant_reg_kernel<L, T, false>), grid, block, lds, s, x, ldx, q, ldq, sx, M,   \
-                         K, wpr);                                                                                 \
+                         K, wpr, fin);                                                                            \
     return launch_status();                                                                                       \
   }
 #define HF_RQ_CASES(L) HF_RQ_CASE(L, 1) HF_RQ_CASE(L, 2) HF_RQ_CASE(L, 3) HF_RQ_CASE(L, 4) HF_RQ_CASE(L, 5)
@@ -180,7 +181,7 @@ int launch_rotate_reg(int lg, int tpw, bool f32, dim3 grid, dim3 block, size_t l
 // Rows of at most 4 * kRqRegMaxTpw tiles held in registers (rotate_quant_reg_kernel): wpr waves of tpw tiles per
 // row, 4 / wpr rows per workgroup. The caller has checked the group, the alignment and M > 0.
 int rotate_rows_in_registers(bool f32, int lg, const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx,
-                             int64_t M, int64_t K, hipStream_t s) {
+                             int64_t M, int64_t K, hipStream_t s, const hf::LrFinish& fin) {
   const int64_t ntiles = (K + hf::kRqTile - 1) / hf::kRqTile;
   const int wpr = (int)((ntiles + hf::kRqRegMaxTpw - 1) / hf::kRqRegMaxTpw);
   const int tpw = (int)((ntiles + wpr - 1) / wpr);
@@ -190,7 +191,7 @@ int rotate_rows_in_registers(bool f32, int lg, const uint16_t* x, int64_t ldx, i
   if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   allow_large_lds();
   return launch_rotate_reg(lg, tpw, f32, dim3((unsigned)blocks), dim3(64 * nw), hf::rotate_quant_reg_lds_bytes(nw),
-                           s, x, ldx, q, ldq, sx, M, (int)K, wpr);
+                           s, x, ldx, q, ldq, sx, M, (int)K, wpr, fin);
 }
 
 int check_gemm_operands(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw, int64_t M, int64_t N,
@@ -296,9 +297,22 @@ int64_t lowrank_ws_bytes(int64_t M, int64_t K, int32_t r) {
   return p.splits > 1 ? (int64_t)p.splits * M * r * 4 : 0;
 }
 
+// Whether lowrank_down_impl with these sizes and workspace runs the split MFMA kernel for at most 64 ranks (the
+// case in which it can leave its partial sums for the layer's rotation kernel to add).
+bool lowrank_split_planned(int64_t M, int64_t K, int32_t r, const void* ws, int64_t ws_bytes) {
+  if (M <= 0 || K <= 0 || r <= 0 || r > hf::kLrRanks) return false;
+  const LrPlan p = lowrank_plan(M, K);
+  const bool ws_ok = ws && aligned(ws, 16) && ws_bytes >= (int64_t)p.splits * M * r * 4;
+  if (lowrank_rows_faster(M, K) || (lowrank_by_rows(M, K) && p.splits > 1 && !ws_ok)) return false;
+  return p.splits > 1 && ws_ok;
+}
+
+// defer: when the split MFMA kernel runs for at most 64 ranks, its partial sums are left in the workspace and
+// described in *defer for the layer's rotation kernel to add (no lowrank_reduce_kernel launch); otherwise
+// defer->part stays null.
 int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int64_t ld_down, uint16_t* u,
                       int64_t ldu, int64_t M, int64_t K, int32_t r, void* ws, int64_t ws_bytes,
-                      hf_stream_t stream) {
+                      hf_stream_t stream, hf::LrFinish* defer = nullptr) {
   if (M < 0 || K <= 0 || r < 0 || ldx < K || ld_down < K || ldu < r) return HF_ERR_ARGUMENT;
   if (M == 0 || r == 0) return HF_OK;
   if (!x || !down || !u) return HF_ERR_ARGUMENT;
@@ -416,7 +430,9 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
 #undef HF_LR_CASE
     int st = launch_status();
     if (st != HF_OK) return st;
-    if (part) {
+    if (part && defer && r <= hf::kLrRanks) {
+      *defer = hf::LrFinish{part, uo, ldu, M, plan.splits, rr};
+    } else if (part) {
       const int64_t n = M * rr;
       hipLaunchKernelGGL(hf::lowrank_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part,
                          plan.splits, uo, ldu, (int)M, rr);
@@ -800,6 +816,66 @@ int int8_linear_impl(const int8_t* q, int64_t ldq, const int8_t* w, int64_t ldw,
 }
 
 
+// hf_rotate_quant's work. fin: the layer's low-rank partial sums, added by the rotation kernels for their rows
+// (the row and register kernels) or by lowrank_reduce_kernel after the rotation; part null: none. dry: only the
+// argument checks (the status the call would return before launching anything).
+int rotate_quant_bf16(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int64_t K,
+                      int32_t group, hipStream_t s, const hf::LrFinish& fin, bool dry) {
+  if (M < 0 || K <= 0 || ldx < K || ldq < K) return HF_ERR_ARGUMENT;
+  if (M == 0) return HF_OK;
+  if (!x || !q || !sx) return HF_ERR_ARGUMENT;
+  const int lg = log4_of(group);
+  if (lg < 0 || K % group) return HF_ERR_GROUP;
+  if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16)) return HF_ERR_ALIGNMENT;
+  int waves = 4;
+  while (waves > 0 && hf::rotate_quant_lds_bytes(waves, (int)std::min<int64_t>(K, 1 << 30)) > (size_t)kMaxLds)
+    waves >>= 1;
+  if (lg < 6 && (waves == 0 || K > 77312)) return HF_ERR_SIZE;
+  if (lg >= 6 && (hf::rotate_quant_wide_lds_bytes((int)std::min<int64_t>(K, 1 << 20)) > (size_t)kMaxLds ||
+                  M >= (int64_t(1) << 31)))
+    return HF_ERR_SIZE;
+  if (dry) return HF_OK;
+  // The low-rank sums for the routes whose kernels do not add them.
+  auto reduce_after = [&](int st) {
+    if (st != HF_OK || !fin.part) return st;
+    const int64_t n = fin.M * fin.r;
+    hipLaunchKernelGGL(hf::lowrank_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, fin.part,
+                       fin.splits, fin.u, fin.ldu, (int)fin.M, fin.r);
+    return launch_status();
+  };
+  if (lg >= 6) return reduce_after(launch_rotate_wide(false, lg, x, ldx, q, ldq, sx, M, K, s));
+  allow_large_lds();
+  const int64_t ntiles = (K + hf::kRqTile - 1) / hf::kRqTile;
+  // Few rows: one workgroup per row, one wave per tile, while the rows fit two rounds of workgroups (the row
+  // buffer and transpose areas take up to 157 KiB per workgroup: at M=1024, K=13824 the register kernel below took
+  // 15.8 us against 20.3; at K=5120, two workgroups per CU, the row kernel stays ahead up to 1024 rows).
+  const int64_t row_wgs_per_cu = std::max<int64_t>(1, kMaxLds / (int64_t)hf::rotate_quant_row_lds_bytes((int)K));
+  if (M <= kRowKernelMaxRows && M <= 2 * row_wgs_per_cu * device_cus() && ntiles <= 14) {
+    const size_t lds = hf::rotate_quant_row_lds_bytes((int)K);
+    const dim3 grid((unsigned)M), block((unsigned)(64 * ntiles));
+    switch (lg) {
+      case 1: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<1>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K, fin); break;
+      case 2: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<2>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K, fin); break;
+      case 3: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<3>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K, fin); break;
+      case 4: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<4>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K, fin); break;
+      default: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<5>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K, fin); break;
+    }
+    return launch_status();
+  }
+  if (ntiles <= 4 * hf::kRqRegMaxTpw) return rotate_rows_in_registers(false, lg, x, ldx, q, ldq, sx, M, K, s, fin);
+  const size_t lds = hf::rotate_quant_lds_bytes(waves, (int)K);
+  const int64_t blocks64 = (M + waves - 1) / waves;
+  const unsigned blocks = (unsigned)std::min<int64_t>(blocks64, int64_t(1) << 30);
+  switch (lg) {
+    case 1: hipLaunchKernelGGL(hf::rotate_quant_kernel<1>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    case 2: hipLaunchKernelGGL(hf::rotate_quant_kernel<2>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    case 3: hipLaunchKernelGGL(hf::rotate_quant_kernel<3>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    case 4: hipLaunchKernelGGL(hf::rotate_quant_kernel<4>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+    default: hipLaunchKernelGGL(hf::rotate_quant_kernel<5>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
+  }
+  return reduce_after(launch_status());
+}
+
 }  // namespace
 
 extern "C" {
@@ -822,48 +898,7 @@ const char* hf_strerror(int status) {
 
 int hf_rotate_quant(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int64_t K,
                     int32_t group, hf_stream_t stream) {
-  if (M < 0 || K <= 0 || ldx < K || ldq < K) return HF_ERR_ARGUMENT;
-  if (M == 0) return HF_OK;
-  if (!x || !q || !sx) return HF_ERR_ARGUMENT;
-  const int lg = log4_of(group);
-  if (lg < 0 || K % group) return HF_ERR_GROUP;
-  if (K % 16 || !aligned(x, 16) || !aligned(q, 16) || (ldx % 8) || (ldq % 16)) return HF_ERR_ALIGNMENT;
-  if (lg >= 6) return launch_rotate_wide(false, lg, x, ldx, q, ldq, sx, M, K, static_cast<hipStream_t>(stream));
-  int waves = 4;
-  while (waves > 0 && hf::rotate_quant_lds_bytes(waves, (int)std::min<int64_t>(K, 1 << 30)) > (size_t)kMaxLds)
-    waves >>= 1;
-  if (waves == 0 || K > 77312) return HF_ERR_SIZE;
-  allow_large_lds();
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t ntiles = (K + hf::kRqTile - 1) / hf::kRqTile;
-  // Few rows: one workgroup per row, one wave per tile, while the rows fit two rounds of workgroups (the row
-  // buffer and transpose areas take up to 157 KiB per workgroup: at M=1024, K=13824 the register kernel below took
-  // 15.8 us against 20.3; at K=5120, two workgroups per CU, the row kernel stays ahead up to 1024 rows).
-  const int64_t row_wgs_per_cu = std::max<int64_t>(1, kMaxLds / (int64_t)hf::rotate_quant_row_lds_bytes((int)K));
-  if (M <= kRowKernelMaxRows && M <= 2 * row_wgs_per_cu * device_cus() && ntiles <= 14) {
-    const size_t lds = hf::rotate_quant_row_lds_bytes((int)K);
-    const dim3 grid((unsigned)M), block((unsigned)(64 * ntiles));
-    switch (lg) {
-      case 1: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<1>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
-      case 2: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<2>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
-      case 3: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<3>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
-      case 4: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<4>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
-      default: hipLaunchKernelGGL(hf::rotate_quant_row_kernel<5>, grid, block, lds, s, x, ldx, q, ldq, sx, (int)K); break;
-    }
-    return launch_status();
-  }
-  if (ntiles <= 4 * hf::kRqRegMaxTpw) return rotate_rows_in_registers(false, lg, x, ldx, q, ldq, sx, M, K, s);
-  const size_t lds = hf::rotate_quant_lds_bytes(waves, (int)K);
-  const int64_t blocks64 = (M + waves - 1) / waves;
-  const unsigned blocks = (unsigned)std::min<int64_t>(blocks64, int64_t(1) << 30);
-  switch (lg) {
-    case 1: hipLaunchKernelGGL(hf::rotate_quant_kernel<1>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
-    case 2: hipLaunchKernelGGL(hf::rotate_quant_kernel<2>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
-    case 3: hipLaunchKernelGGL(hf::rotate_quant_kernel<3>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
-    case 4: hipLaunchKernelGGL(hf::rotate_quant_kernel<4>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
-    default: hipLaunchKernelGGL(hf::rotate_quant_kernel<5>, dim3(blocks), dim3(64 * waves), lds, s, x, ldx, q, ldq, sx, M, (int)K); break;
-  }
-  return launch_status();
+  return rotate_quant_bf16(x, ldx, q, ldq, sx, M, K, group, static_cast<hipStream_t>(stream), hf::LrFinish{}, false);
 }
 
 int hf_rotate_quant_ex(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* sx, int64_t M, int64_t K,
@@ -881,7 +916,7 @@ int hf_rotate_quant_ex(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, f
   if (lg >= 6) return launch_rotate_wide(true, lg, x, ldx, q, ldq, sx, M, K, s);
   // Up to 20 tiles the row stays in registers and x is read once; wider rows take the two-pass kernel below.
   if ((K + hf::kRqTile - 1) / hf::kRqTile <= 4 * hf::kRqRegMaxTpw)
-    return rotate_rows_in_registers(true, lg, x, ldx, q, ldq, sx, M, K, s);
+    return rotate_rows_in_registers(true, lg, x, ldx, q, ldq, sx, M, K, s, hf::LrFinish{});
   constexpr int waves = 4;
   const size_t lds = hf::rotate_quant_f32_recip_lds_bytes(waves);
   const unsigned blocks = (unsigned)std::min<int64_t>((M + waves - 1) / waves, int64_t(1) << 30);
@@ -1066,6 +1101,21 @@ int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, i
   int st = HF_OK;
   if (!quantized && r > 0 && arithmetic == HF_ROTATE_BF16_DIV && group <= 1024 && rotate_lowrank_by_rows(M, K)) {
     st = rotate_lowrank_rows(x, ldx, q, K, sx, down, ld_down, u, r, M, K, r, group, stream);
+    if (st != HF_OK) return st;
+  } else if (!quantized && r > 0 && arithmetic == HF_ROTATE_BF16_DIV && lowrank_split_planned(M, K, r, ws, ws_bytes)) {
+    // The low-rank projection splits K: it runs first and the rotation kernel adds its partial sums for the rows it
+    // rotates (one launch fewer; the same sums in the same order: config 1's layer 37.9 -> 35.1 us, M=1024, N=K=5120
+    // 59.9 -> 57.4 us). Without a split the projection stays the last reader of x (its loads keep x out of the
+    // Infinity Cache, over the codes the GEMM reads next): run first, it cost 0.6-0.8 % at M=32768 and M=256. The
+    // rotation's arguments are checked before anything runs. The low-rank partials and the GEMM's partial planes
+    // share the workspace: they are used one after the other.
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    st = rotate_quant_bf16(x, ldx, q, K, sx, M, K, group, s, hf::LrFinish{}, true);
+    if (st != HF_OK) return st;
+    hf::LrFinish fin{};
+    st = lowrank_down_impl(x, ldx, down, ld_down, u, r, M, K, r, ws, ws_bytes, stream, &fin);
+    if (st != HF_OK) return st;
+    st = rotate_quant_bf16(x, ldx, q, K, sx, M, K, group, s, fin, false);
     if (st != HF_OK) return st;
   } else {
     if (!quantized) {

@@ -413,13 +413,10 @@ __global__ __launch_bounds__(512, 1) void lowrank_down_band_kernel(const uint16_
 
 constexpr int kMaxSplits = 32;  // K chunks of a split launch, at most
 
-// u[m, j] = bf16(sum_s part[s][m][j]): the planes added in a fixed order, one rounding (round to nearest even).
-__global__ __launch_bounds__(256) void lowrank_reduce_kernel(const float* __restrict__ part, int splits,
-                                                             uint16_t* __restrict__ u, int64_t ldu, int M, int r) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)M * r) return;
-  const int m = (int)(i / r), j = (int)(i % r);
-  // All loads first (splits <= kMaxSplits), then the adds in plane order.
+// bf16(sum_s part[s][i]) for element i = m r + j of the [splits][M][r] partial sums: the planes added in a fixed
+// order from plane 0, one rounding (round to nearest even). All loads first (splits <= kMaxSplits), then the adds.
+__device__ __forceinline__ uint16_t lr_reduce_value(const float* __restrict__ part, int splits, int64_t M, int r,
+                                                    int64_t i) {
   float p[kMaxSplits];
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) p[s] = s < splits ? part[(int64_t)s * M * r + i] : 0.0f;
@@ -427,7 +424,31 @@ __global__ __launch_bounds__(256) void lowrank_reduce_kernel(const float* __rest
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s)
     if (s < splits) v += p[s];
-  u[(int64_t)m * ldu + j] = (uint16_t)f32_to_bf16_rne(v);
+  return (uint16_t)f32_to_bf16_rne(v);
+}
+
+// u[m, j] = bf16(sum_s part[s][m][j]) (lr_reduce_value).
+__global__ __launch_bounds__(256) void lowrank_reduce_kernel(const float* __restrict__ part, int splits,
+                                                             uint16_t* __restrict__ u, int64_t ldu, int M, int r) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)M * r) return;
+  const int m = (int)(i / r), j = (int)(i % r);
+  u[(int64_t)m * ldu + j] = lr_reduce_value(part, splits, M, r, i);
+}
+
+// The same sums added by the rotation kernels of a layer for the rows they rotate, in place of a launch of
+// lowrank_reduce_kernel between the two passes over x (the low-rank projection then runs first). `part` null: none.
+struct LrFinish {
+  const float* part;  // [splits][M][r] fp32 partial sums
+  uint16_t* u;        // [M, ldu] bf16
+  int64_t ldu;
+  int64_t M;
+  int splits, r;      // r <= 64: one lane per rank
+};
+
+// Row `row`'s r sums, lane j < r taking rank j.
+__device__ __forceinline__ void lr_finish_row(const LrFinish& f, int64_t row, int lane) {
+  if (lane < f.r) f.u[row * f.ldu + lane] = lr_reduce_value(f.part, f.splits, f.M, f.r, row * f.r + lane);
 }
 
 // Few rows: a workgroup per row and group of 8 ranks, which needs no second pass. The MFMA kernel above keeps 32 rows

@@ -342,12 +342,14 @@ __device__ __forceinline__ void rotate_quant_row(const uint16_t* __restrict__ x,
   quantize_tile(rowbuf, t, K, lane, rs, q + row * ldq);  // this wave's own tile: its writes are visible to it
 }
 
+// `fin`: the layer's low-rank partial sums of this row, added by the row's first wave (LrFinish; part null: none).
 template <int LOG4G>
 __global__ __launch_bounds__(1024) void rotate_quant_row_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                 int8_t* __restrict__ q, int64_t ldq,
-                                                                float* __restrict__ s, int K) {
+                                                                float* __restrict__ s, int K, LrFinish fin) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   rotate_quant_row<LOG4G>(x, ldx, q, ldq, s, K, blockIdx.x, smem);
+  if (fin.part && threadIdx.x < 64) lr_finish_row(fin, blockIdx.x, threadIdx.x);
 }
 
 // The row rotation and the row-wise low-rank down projection (lowrank_row_block) of the same few rows in one launch:
@@ -423,7 +425,7 @@ size_t rotate_quant_reg_lds_bytes(int waves) { return (size_t)waves * kRqScratch
 template <int LOG4G, int TPW, bool F32>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TPW == kRqRegMaxTpw ? (LOG4G == 5 ? 3 : 4) : 1)))
 void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q, int64_t ldq,
-                             float* __restrict__ s, int64_t M, int K, int wpr) {
+                             float* __restrict__ s, int64_t M, int K, int wpr, LrFinish fin) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar addressing
@@ -500,6 +502,8 @@ void rotate_quant_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t
       if (base < K) quantize_store_tile<LOG4G>(held[i], rs, base, K, lane, stage, qrow);
     }
   }
+  // The layer's low-rank partial sums of this row (LrFinish; part null: none), added by the row's first wave.
+  if (fin.part && part == 0) lr_finish_row(fin, row, lane);
 }
 
 // The arithmetic of the reference's GPU kernels (rotate_quant_kernel / rotate_quant_factored_kernel,
@@ -649,9 +653,9 @@ template __global__ void rotate_quant_wide_kernel<true>(const uint16_t*, int64_t
 
 #define HF_RQ_REG(L, T)                                                                                            \
   template __global__ void rotate_quant_reg_kernel<L, T, false>(const uint16_t*, int64_t, int8_t*, int64_t, float*,\
-                                                                int64_t, int, int);                               \
+                                                                int64_t, int, int, LrFinish);                     \
   template __global__ void rotate_quant_reg_kernel<L, T, true>(const uint16_t*, int64_t, int8_t*, int64_t, float*, \
-                                                               int64_t, int, int);
+                                                               int64_t, int, int, LrFinish);
 #define HF_RQ_REG_ALL(L) HF_RQ_REG(L, 1) HF_RQ_REG(L, 2) HF_RQ_REG(L, 3) HF_RQ_REG(L, 4) HF_RQ_REG(L, 5)
 HF_RQ_REG_ALL(1)
 HF_RQ_REG_ALL(2)
@@ -666,11 +670,16 @@ template __global__ void rotate_quant_kernel<2>(const uint16_t*, int64_t, int8_t
 template __global__ void rotate_quant_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
 template __global__ void rotate_quant_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
 template __global__ void rotate_quant_kernel<5>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int64_t, int);
-template __global__ void rotate_quant_row_kernel<1>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
-template __global__ void rotate_quant_row_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
-template __global__ void rotate_quant_row_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
-template __global__ void rotate_quant_row_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
-template __global__ void rotate_quant_row_kernel<5>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int);
+template __global__ void rotate_quant_row_kernel<1>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int,
+                                                    LrFinish);
+template __global__ void rotate_quant_row_kernel<2>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int,
+                                                    LrFinish);
+template __global__ void rotate_quant_row_kernel<3>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int,
+                                                    LrFinish);
+template __global__ void rotate_quant_row_kernel<4>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int,
+                                                    LrFinish);
+template __global__ void rotate_quant_row_kernel<5>(const uint16_t*, int64_t, int8_t*, int64_t, float*, int,
+                                                    LrFinish);
 #define HF_RQ_LR_ROW(G)                                                                                             \
   template __global__ void rotate_lowrank_row_kernel<G>(const uint16_t*, int64_t, int8_t*, int64_t, float*,         \
                                                         const uint16_t*, int64_t, uint16_t*, int64_t, int, int, int, \
