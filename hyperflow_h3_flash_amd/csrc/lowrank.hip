@@ -415,16 +415,23 @@ constexpr int kMaxSplits = 32;  // K chunks of a split launch, at most
 
 // bf16(sum_s part[s][i]) for element i = m r + j of the [splits][M][r] partial sums: the planes added in a fixed
 // order from plane 0, one rounding (round to nearest even). All loads first (splits <= kMaxSplits), then the adds.
-__device__ __forceinline__ uint16_t lr_reduce_value(const float* __restrict__ part, int splits, int64_t M, int r,
-                                                    int64_t i) {
-  float p[kMaxSplits];
+__device__ __forceinline__ void lr_reduce_load(const float* __restrict__ part, int splits, int64_t M, int r, int64_t i,
+                                               float (&p)[kMaxSplits]) {
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) p[s] = s < splits ? part[(int64_t)s * M * r + i] : 0.0f;
+}
+__device__ __forceinline__ uint16_t lr_reduce_sum(const float (&p)[kMaxSplits], int splits) {
   float v = 0.0f;
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s)
     if (s < splits) v += p[s];
   return (uint16_t)f32_to_bf16_rne(v);
+}
+__device__ __forceinline__ uint16_t lr_reduce_value(const float* __restrict__ part, int splits, int64_t M, int r,
+                                                    int64_t i) {
+  float p[kMaxSplits];
+  lr_reduce_load(part, splits, M, r, i, p);
+  return lr_reduce_sum(p, splits);
 }
 
 // u[m, j] = bf16(sum_s part[s][m][j]) (lr_reduce_value).

@@ -342,14 +342,18 @@ __device__ __forceinline__ void rotate_quant_row(const uint16_t* __restrict__ x,
   quantize_tile(rowbuf, t, K, lane, rs, q + row * ldq);  // this wave's own tile: its writes are visible to it
 }
 
-// `fin`: the layer's low-rank partial sums of this row, added by the row's first wave (LrFinish; part null: none).
+// `fin`: the layer's low-rank partial sums of this row, added by the row's first wave (LrFinish; part null: none);
+// their loads are issued before the rotation so they land while it runs.
 template <int LOG4G>
 __global__ __launch_bounds__(1024) void rotate_quant_row_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                 int8_t* __restrict__ q, int64_t ldq,
                                                                 float* __restrict__ s, int K, LrFinish fin) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const bool lr = fin.part && threadIdx.x < fin.r;
+  float p[kMaxSplits];
+  if (lr) lr_reduce_load(fin.part, fin.splits, fin.M, fin.r, (int64_t)blockIdx.x * fin.r + threadIdx.x, p);
   rotate_quant_row<LOG4G>(x, ldx, q, ldq, s, K, blockIdx.x, smem);
-  if (fin.part && threadIdx.x < 64) lr_finish_row(fin, blockIdx.x, threadIdx.x);
+  if (lr) fin.u[(int64_t)blockIdx.x * fin.ldu + threadIdx.x] = lr_reduce_sum(p, fin.splits);
 }
 
 // The row rotation and the row-wise low-rank down projection (lowrank_row_block) of the same few rows in one launch:
