@@ -84,6 +84,30 @@ def test_one_call_forward_is_the_composed_forward(m, k, n, rank, bias, activatio
     np.testing.assert_array_equal(bits_of(fast), bits_of(slow))
 
 
+@pytest.mark.parametrize("m,k,n,group,rank", [
+    (700, 2048, 384, 256, 1),      # the row rotation kernel adds the sums; rank 1
+    (2000, 3072, 640, 256, 64),    # the register rotation kernel adds them
+    (3000, 1024, 256, 256, 48),    # the register kernel, one tile per row
+    (4096, 5120, 512, 256, 32),
+    (1100, 24576, 256, 256, 64),   # rows past 20 tiles: the reduce runs after the rotation kernel
+    (1500, 8192, 256, 4096, 64),   # group 4096: the wide rotation kernel, the reduce after it
+])
+def test_one_call_split_low_rank_sums_in_the_rotation(m, k, n, group, rank):
+    """Layers whose low-rank projection splits K: the one library call runs the projection first and the rotation
+    adds its partial sums (or, for rotation kernels that do not, a reduce launch after them); the result equals the
+    composed calls (rotation, projection with its own reduce, GEMM) bit for bit."""
+    from hyperflow_h3_flash_amd import _native
+
+    lib = _native.library()
+    assert lib.hf_lowrank_down_ws_bytes(m, k, rank) > 0  # the projection splits K at this size
+    layer = make_layer(k, n, group, rank, False, seed=m + k)
+    x = torch.randn(m, k, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        fast = layer(x)
+        slow = composed(lambda: layer(x))
+    np.testing.assert_array_equal(bits_of(fast), bits_of(slow))
+
+
 def test_one_call_forward_shares_the_quantized_input():
     """q/k/v on one input: the first (keep_input) quantizes, the next two reuse its codes; the outputs equal those of
     layers that each quantize for themselves, and nothing outlives the projections."""
