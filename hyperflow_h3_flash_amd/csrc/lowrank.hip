@@ -57,8 +57,8 @@ __device__ __forceinline__ void lr_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t oo
 }
 
 // Split K (few rows): blockIdx.y = s covers K elements [s * k_chunk, (s + 1) * k_chunk) and writes its fp32 partial
-// sums to plane s of `part` ([splits][M][r]); lowrank_reduce_kernel adds the planes and rounds to bf16. Unsplit
-// launches (gridDim.y == 1, part == nullptr) write u directly.
+// sums to plane s of `part` ([splits][M][r]); lowrank_reduce_kernel, or in a layer the rotation kernel (LrFinish),
+// adds the planes and rounds to bf16. Unsplit launches (gridDim.y == 1, part == nullptr) write u directly.
 template <int RB, int NW = 4>
 __global__ __launch_bounds__(64 * NW, 1) void lowrank_down_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                   const uint16_t* __restrict__ down, int64_t ldd,

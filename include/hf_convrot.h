@@ -186,7 +186,9 @@ int hf_convrot_linear(const uint16_t* x, int64_t ldx, const int8_t* w, int64_t l
  *                   int8.py:150-159), and x is read only by the low-rank term;
  * then, when r > 0, hf_lowrank_down_ws(x -> u [M, r] (ldu = r)), then hf_int8_linear_act_ws(q, ..., activation ->
  * y). `ws` serves both split-K passes (one after the other): hf_convrot_linear_ws_bytes gives its size for these
- * sizes, rank and activation (a NULL or smaller workspace runs the unsplit kernels). Same rules as the calls it makes.
+ * sizes, rank and activation (a NULL or smaller workspace runs the unsplit kernels). Same rules as the calls it makes,
+ * and the same results bit for bit; when the low-rank projection splits K (quantized == 0, HF_ROTATE_BF16_DIV, r <= 64)
+ * it runs before the rotation, whose kernel then adds its partial sums (one launch fewer).
  */
 int64_t hf_convrot_linear_ws_bytes(int64_t M, int64_t N, int64_t K, int32_t r, int32_t activation);
 int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, int32_t quantized, int32_t arithmetic,
