@@ -297,14 +297,32 @@ int64_t lowrank_ws_bytes(int64_t M, int64_t K, int32_t r) {
   return p.splits > 1 ? (int64_t)p.splits * M * r * 4 : 0;
 }
 
+// The first choice of lowrank_down_impl (before its wide-rank routes, which need many rows and one pass over K): the
+// row kernel, or the MFMA kernel with this K plan. A split needs its workspace (the fp32 partial sums of the first
+// 64 ranks); without it the rows are still the faster choice where they apply, else the MFMA kernel takes K in one
+// pass.
+struct LrRoute {
+  bool by_rows;
+  LrPlan plan;
+};
+LrRoute lowrank_route(int64_t M, int64_t K, int32_t r, const void* ws, int64_t ws_bytes) {
+  LrRoute rt{lowrank_rows_faster(M, K), lowrank_plan(M, K)};
+  const bool ws_ok = ws && aligned(ws, 16) &&
+                     ws_bytes >= (int64_t)rt.plan.splits * M * std::min<int32_t>(r, hf::kLrRanks) * 4;
+  if (rt.plan.splits > 1 && !ws_ok) {
+    if (lowrank_by_rows(M, K)) rt.by_rows = true;
+    rt.plan = LrPlan{};
+    rt.plan.k_chunk = (int)K;
+  }
+  return rt;
+}
+
 // Whether lowrank_down_impl with these sizes and workspace runs the split MFMA kernel for at most 64 ranks (the
 // case in which it can leave its partial sums for the layer's rotation kernel to add).
 bool lowrank_split_planned(int64_t M, int64_t K, int32_t r, const void* ws, int64_t ws_bytes) {
   if (M <= 0 || K <= 0 || r <= 0 || r > hf::kLrRanks) return false;
-  const LrPlan p = lowrank_plan(M, K);
-  const bool ws_ok = ws && aligned(ws, 16) && ws_bytes >= (int64_t)p.splits * M * r * 4;
-  if (lowrank_rows_faster(M, K) || (lowrank_by_rows(M, K) && p.splits > 1 && !ws_ok)) return false;
-  return p.splits > 1 && ws_ok;
+  const LrRoute rt = lowrank_route(M, K, r, ws, ws_bytes);
+  return !rt.by_rows && rt.plan.splits > 1;
 }
 
 // defer: when the split MFMA kernel runs for at most 64 ranks, its partial sums are left in the workspace and
@@ -320,14 +338,8 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
     return HF_ERR_ALIGNMENT;
   if (M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HF_ERR_SIZE;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  bool by_rows = lowrank_rows_faster(M, K);
-  if (!by_rows && lowrank_by_rows(M, K)) {
-    // The split MFMA kernel wins here only with its workspace; without one the rows are still the faster choice.
-    const LrPlan p = lowrank_plan(M, K);
-    by_rows = p.splits > 1 && (!ws || !aligned(ws, 16) ||
-                               ws_bytes < (int64_t)p.splits * M * std::min<int32_t>(r, hf::kLrRanks) * 4);
-  }
-  if (by_rows) {
+  const LrRoute route = lowrank_route(M, K, r, ws, ws_bytes);
+  if (route.by_rows) {
     const int64_t waves = (K + 1023) / 1024, groups = (r + hf::kLrRowRanks - 1) / hf::kLrRowRanks;
     const int64_t blocks = hf::lowrank_row_blocks(M, r);
     if (blocks >= (int64_t(1) << 31)) return HF_ERR_SIZE;
@@ -338,12 +350,7 @@ int lowrank_down_impl(const uint16_t* x, int64_t ldx, const uint16_t* down, int6
   if (2 * hf::kLrMaxRows * ldx >= (int64_t(1) << 31) || 2 * hf::kLrRanks * ld_down >= (int64_t(1) << 31))
     return HF_ERR_SIZE;
   allow_large_lds();
-  LrPlan plan = lowrank_plan(M, K);
-  if (plan.splits > 1 && (!ws || ws_bytes < (int64_t)plan.splits * M * std::min<int32_t>(r, hf::kLrRanks) * 4 ||
-                          !aligned(ws, 16))) {
-    plan = LrPlan{};  // no (or too small a) workspace: one pass over K
-    plan.k_chunk = (int)K;
-  }
+  const LrPlan plan = route.plan;
   if (plan.splits == 1 && r > 128 && K >= 4096 && 8 * ((M + hf::kLbRows - 1) / hf::kLbRows) >= 7 * device_cus() &&
       8 * ((M + hf::kLbRows - 1) / hf::kLbRows) <= 8 * device_cus()) {
     // Ranks past 128 with 160-row blocks filling 7/8 to all of the CUs: lowrank_down_band_kernel, 256 ranks per pass
