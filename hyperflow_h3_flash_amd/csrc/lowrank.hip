@@ -275,34 +275,40 @@ template __global__ void lowrank_down_wide_kernel<4>(const uint16_t*, int64_t, c
 template __global__ void lowrank_down_wide_kernel<5>(const uint16_t*, int64_t, const uint16_t*, int64_t, uint16_t*,
                                                      int64_t, int, int, int);
 
-// lowrank_down_wide_kernel's tile (160 rows of x against 256 ranks per pass) on 8 waves instead of 10, with x and
-// down in rings of their own. Wave w multiplies all five 32-row blocks against ranks 32 w .. 32 w + 31 (five MFMA
-// blocks, one down fragment and five x fragments per K step), so every SIMD holds two waves; with ten, two SIMDs held
-// three and set the pace. x streams from HBM and its rate follows the bytes in flight (a 52 KiB stage of which the
-// 256-rank down slab takes 32 KiB left one stage of x in flight: ~2.8 TB/s), so x gets a 4-slot ring (three stages
-// ahead) loaded by waves 0-3 and down, read from L2, a 2-slot ring (one stage ahead) loaded by waves 4-7: each
-// wave's in-order vmcnt wait covers only its own ring. The fragments of the next K step are read while the current
-// one's MFMAs run. Each u element is the same sum in the same order as lowrank_down_wide_kernel's (and the 64-rank
-// passes'): K ascending in 16-element MFMA steps, down as the first operand.
+// lowrank_down_wide_kernel's tile (160 rows of x against 256 ranks per pass) on 8 waves instead of 10. Wave w
+// multiplies all five 32-row blocks against ranks 32 w .. 32 w + 31 (five MFMA blocks, one down fragment and five x
+// fragments per K step), so every SIMD holds two waves; with ten, two SIMDs held three and set the pace. x streams
+// from HBM through a 4-slot LDS ring, loaded three stages ahead; the 256-rank down slab, read from L2, takes two
+// 32 KiB LDS slots and is staged through registers: each stage is loaded three stages ahead into one of three
+// register buffers and written into its LDS slot one stage ahead, which gives it two stages of lead where an LDS-DMA
+// ring in the same space gave one (M=37710: K=14336, r=384 597 -> 516 us, K=8192, r=320 353 -> 309 us, K=5376, r=512
+// 267 -> 251 us, r=192 122 -> 110 us; within 1 % at K=14336, r=256). Every wave issues the same memory operations
+// in the same order (per stage 4 down loads into registers, then 3 x loads; x's 20 blocks of a stage go 3 to a wave
+// and the last four read zeros into a sink past the rings), so the waits the compiler places before the register
+// writes to LDS are exact for every wave and never include the x loads of that stage. The fragments of the next K
+// step are read while the current one's MFMAs run. Each u element is the same sum in the same order as
+// lowrank_down_wide_kernel's (and the 64-rank passes'): K ascending in 16-element MFMA steps, down as the first
+// operand.
 constexpr int kLbRows = 160;
 constexpr int kLbXBytes = kLbRows * kLrStageK * 2;   // 20 KiB a stage of x
 constexpr int kLbDBytes = kLwRanks * kLrStageK * 2;  // 32 KiB a stage of down
 constexpr int kLbXSlots = 4, kLbDSlots = 2;
-constexpr int kLbLds = kLbXSlots * kLbXBytes + kLbDSlots * kLbDBytes;  // 144 KiB
-constexpr int kLbXLoads = kLbRows / 8 / 4;   // 5 per x wave and stage
-constexpr int kLbDLoads = kLwRanks / 8 / 4;  // 8 per down wave and stage
+constexpr int kLbRings = kLbXSlots * kLbXBytes + kLbDSlots * kLbDBytes;  // 144 KiB
+constexpr int kLbLds = kLbRings + 1024;                                  // + the sink of the x loads past a stage
+constexpr int kLbXLoads = 3;                 // x blocks (8 rows) per wave and stage: 24 >= 20
+constexpr int kLbDLoads = kLwRanks / 8 / 8;  // down blocks per wave and stage: 4
 
 __global__ __launch_bounds__(512, 1) void lowrank_down_band_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                    const uint16_t* __restrict__ down, int64_t ldd,
                                                                    uint16_t* __restrict__ u, int64_t ldu, int M, int K,
                                                                    int r) {
   static_assert(kLbLds <= 160 * 1024, "rings exceed the LDS");
+  static_assert(8 * kLbXLoads >= kLbRows / 8, "x blocks");
   extern __shared__ __attribute__((aligned(1024))) unsigned char lb_smem_raw[];
   unsigned char HF_LDS* smem = (unsigned char HF_LDS*)lb_smem_raw;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane & 31, half = lane >> 5;
-  const bool xw = wave < 4;  // x loader (waves 0-3) or down loader (waves 4-7)
   const int m0 = blockIdx.x * kLbRows;
   const int rows_m = min(kLbRows, M - m0);
   const uint32_t ldx_bytes = (uint32_t)ldx * 2u, ldd_bytes = (uint32_t)ldd * 2u;
@@ -311,13 +317,40 @@ __global__ __launch_bounds__(512, 1) void lowrank_down_band_kernel(const uint16_
   const __amdgpu_buffer_rsrc_t rd = make_rsrc(down, bytes_d);
   auto xslot = [&](int t) { return smem + (t % kLbXSlots) * kLbXBytes; };
   auto dslot = [&](int t) { return smem + kLbXSlots * kLbXBytes + (t % kLbDSlots) * kLbDBytes; };
-  // This wave's loads of stage t: x blocks 5 w .. 5 w + 4, or down blocks 8 (w - 4) .. 8 (w - 4) + 7 (8 rows each;
-  // stages past the end read zeros).
+  // This wave's x loads of stage t (LDS-DMA): blocks 3 w .. 3 w + 2 in lr_load's LDS layout; rows past the block and
+  // stages past the end read zeros, and blocks past the stage's 20 go to the sink.
   auto issue_x = [&](int t) {
-    lr_load<kLbXLoads, kCpolStream>(rx, bytes_x, ldx_bytes, rows_m, t * kLrStageK, K, xslot(t), wave * kLbXLoads, lane);
+    const int k0 = t * kLrStageK;
+#pragma unroll
+    for (int i = 0; i < kLbXLoads; ++i) {
+      const int blk = wave * kLbXLoads + i;
+      const int row = blk * 8 + (lane >> 3);
+      const int c = lr_swizzle(row, lane & 7);
+      const int k = k0 + c * 8;
+      const bool in = blk < kLbRows / 8;
+      const uint32_t voff = (in & (row < rows_m) & (k < K)) ? (uint32_t)row * ldx_bytes + (uint32_t)k * 2u : bytes_x;
+      unsigned char HF_LDS* dst = in ? xslot(t) + blk * 1024 : smem + kLbRings;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (void HF_LDS*)dst, 16, voff, 0, 0, kCpolStream);
+    }
   };
-  auto issue_d = [&](int t) {
-    lr_load<kLbDLoads>(rd, bytes_d, ldd_bytes, r, t * kLrStageK, K, dslot(t), (wave - 4) * kLbDLoads, lane);
+  // This wave's down blocks 4 w .. 4 w + 3 of stage t into registers, and from registers into the stage's LDS slot,
+  // in lr_load's layout (lane l of a block: row 8 blk + l / 8, chunk lr_swizzle(row, l % 8)).
+  auto load_d = [&](v4u (&b)[kLbDLoads], int t) {
+#pragma unroll
+    for (int i = 0; i < kLbDLoads; ++i) {
+      const int blk = wave * kLbDLoads + i;
+      const int row = blk * 8 + (lane >> 3);
+      const int c = lr_swizzle(row, lane & 7);
+      const int k = t * kLrStageK + c * 8;
+      const uint32_t voff = ((row < r) & (k < K)) ? (uint32_t)row * ldd_bytes + (uint32_t)k * 2u : bytes_d;
+      b[i] = __builtin_amdgcn_raw_buffer_load_b128(rd, voff, 0, 0);
+    }
+  };
+  auto write_d = [&](const v4u (&b)[kLbDLoads], int t) {
+    unsigned char HF_LDS* dst = dslot(t);
+#pragma unroll
+    for (int i = 0; i < kLbDLoads; ++i)
+      *reinterpret_cast<v4u HF_LDS*>(dst + (wave * kLbDLoads + i) * 1024 + lane * 16) = b[i];
   };
 
   v16f acc[5];
@@ -325,12 +358,19 @@ __global__ __launch_bounds__(512, 1) void lowrank_down_band_kernel(const uint16_
   for (int rb = 0; rb < 5; ++rb) acc[rb] = (v16f){0};
   const bool live = wave * 32 < r;  // a wave whose ranks are all past r only loads
   const int nst = (K + kLrStageK - 1) / kLrStageK;
-  if (xw) {
-#pragma unroll
-    for (int t = 0; t < kLbXSlots - 1; ++t) issue_x(t);
-  } else {
-    issue_d(0);
-  }
+  // Three register buffers of down stages. A stage's down loads go before its x loads (held there by the scheduling
+  // barriers), so waiting for them before their LDS writes never waits for the x loads of the same stage.
+  v4u db0[kLbDLoads], db1[kLbDLoads], db2[kLbDLoads];
+  load_d(db0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_x(0);
+  load_d(db1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_x(1);
+  load_d(db2, 2);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_x(2);
+  write_d(db0, 0);
   const int drow = wave * 32 + sub;
   struct Frags {
     v8bf d;
@@ -350,19 +390,18 @@ __global__ __launch_bounds__(512, 1) void lowrank_down_band_kernel(const uint16_
     for (int rb = 0; rb < 5; ++rb) acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.d, f.x[rb], acc[rb], 0, 0, 0);
   };
   Frags f0, f1;
-  for (int t = 0; t < nst; ++t) {
-    // Stage t has landed for this wave's ring (x waves: stages t + 1 and t + 2 still in flight; down waves: nothing)
-    // and its reads of stage t - 1 have returned; the barrier makes that true for every wave, so the slots of stage
-    // t - 1 take x stage t + 3 and down stage t + 1.
-    if (xw)
-      asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (xw)
-      issue_x(t + kLbXSlots - 1);
-    else
-      issue_d(t + 1);
-    if (!live) continue;
+  // Stage t, with down stage t + 1 in register buffer wbuf and buffer lbuf free (its stage, t, is in LDS).
+  auto body = [&](int t, v4u (&wbuf)[kLbDLoads], v4u (&lbuf)[kLbDLoads]) {
+    // x stage t has landed once at most the next two stages' 2 x (4 + 3) operations are in flight, and this wave's
+    // LDS writes of down stage t are done; the barrier makes both true for every wave and frees the slots of stage
+    // t - 1, which take down stage t + 1 (from registers) and x stage t + 3.
+    static_assert(2 * (kLbDLoads + kLbXLoads) == 14, "the wait count below");
+    asm volatile("s_waitcnt vmcnt(14) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    write_d(wbuf, t + 1);
+    load_d(lbuf, t + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    issue_x(t + 3);
+    if (!live) return;
     const unsigned char HF_LDS* xs = xslot(t);
     const unsigned char HF_LDS* ds = dslot(t);
     read(f0, xs, ds, 0);
@@ -389,7 +428,17 @@ __global__ __launch_bounds__(512, 1) void lowrank_down_band_kernel(const uint16_
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);
     __builtin_amdgcn_sched_barrier(0);
+  };
+  // Stage t writes buffer (t + 1) % 3 and loads buffer t % 3. Whole rounds of three stages in the loop (so every path
+  // through it runs all three and the compiler's waits stay exact), then the last one or two.
+  int t = 0;
+  for (; t + 3 <= nst; t += 3) {
+    body(t, db1, db0);
+    body(t + 1, db2, db1);
+    body(t + 2, db0, db2);
   }
+  if (t < nst) body(t, db1, db0);
+  if (t + 1 < nst) body(t + 1, db2, db1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // zero-fill loads past the end may still be landing
   if (!live) return;
 #pragma unroll
