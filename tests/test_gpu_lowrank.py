@@ -184,7 +184,8 @@ def test_device_layer_without_the_library_raises(monkeypatch):
 
 @pytest.mark.parametrize("m,k,r", [(16500, 1040, 72), (20000, 5376, 256), (17000, 2048, 200), (33000, 1024, 320),
                                    (33000, 1024, 512), (37710, 5376, 128), (37710, 5376, 256), (40000, 2064, 200),
-                                   (37710, 5376, 200), (37710, 14336, 256), (37710, 5376, 512)])
+                                   (37710, 5376, 200), (37710, 14336, 256), (37710, 5376, 512),
+                                   (37710, 4112, 136), (36000, 4224, 264), (40960, 4288, 392)])
 def test_wide_rank_down_projection(oracle_lib, m, k, r):
     """Ranks past 64 with more rows than half the CUs' 128-row workgroups cover (no K split) take 256 ranks per pass
     over x (lowrank_down_wide_kernel): the same sums, in the same order, as 64-rank passes of the unsplit rank-64
@@ -195,7 +196,10 @@ def test_wide_rank_down_projection(oracle_lib, m, k, r):
     512; M=40000, r=200 with a partial column tile and K=2064, not a multiple of the 64-element stage) the persistent
     tile kernel's bf16 product runs instead, and past r=128 with K >= 4096 and 160-row blocks filling 7/8 of the CUs
     (M=37710: r=200 with seven live rank blocks of eight, r=256, r=512 in two passes, K=5376 and 14336) the 8-wave
-    kernel with separate x and down rings, all with the same summation order."""
+    kernel with the down slab staged through registers, all with the same summation order. Its last three cases end
+    the stage loop on each of the three register buffers (65, 66 and 67 stages of 64 elements, the first with a
+    partial last stage and a partial last row block), with 136, 264 and 392 ranks (passes whose last live wave holds
+    only 8 of its 32 ranks)."""
     from hyperflow_h3_flash_amd import _native
     from hyperflow_h3_flash_amd.int8 import _stream, lowrank_down
 
