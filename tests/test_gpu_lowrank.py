@@ -223,3 +223,29 @@ def test_wide_rank_down_projection(oracle_lib, m, k, r):
     exact_sum, mag = xf @ df.T, np.abs(xf) @ np.abs(df).T
     assert (np.abs(got - exact_sum) <= 2.0**-8 * np.abs(exact_sum) + (1 + 2.0**-8) * k * 2.0**-24 * mag).all()
     assert (bits_of(u[rows]) == oracle_lib.lowrank_down(xs, ds)).mean() > 0.98
+
+
+@pytest.mark.parametrize("m,k,r,px,pd,pu", [(37710, 4112, 136, 16, 24, 16), (37710, 5376, 256, 64, 8, 8),
+                                            (33000, 1024, 320, 8, 8, 8)])
+def test_wide_rank_down_projection_with_padded_strides(m, k, r, px, pd, pu):
+    """The wide-rank routes (the 8-wave kernel at M=37710, the persistent tiles at M=33000) with x, down and u in
+    padded rows: bitwise the result on contiguous copies, and u's padding columns untouched."""
+    from hyperflow_h3_flash_amd import _native
+    from hyperflow_h3_flash_amd.int8 import _stream
+
+    lib = _native.library()
+    print(f"padded wide-rank low-rank down M={m} K={k} r={r} pads {px} {pd} {pu}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(m + k + r)
+    xs = (torch.randn(m, k + px, device=DEV, generator=gen) * 2.0).to(torch.bfloat16)
+    ds = (torch.randn(r, k + pd, device=DEV, generator=gen) * 0.05).to(torch.bfloat16)
+    us = torch.full((m, r + pu), -1.0, device=DEV, dtype=torch.bfloat16)
+    x, d = xs[:, :k].contiguous(), ds[:, :k].contiguous()
+    u = torch.empty(m, r, device=DEV, dtype=torch.bfloat16)
+    nb = lib.hf_lowrank_down_ws_bytes(m, k, r)
+    ws = torch.empty(max(nb, 1), device=DEV, dtype=torch.uint8)
+    for xx, ldx, dd, ldd, uu, ldu in ((xs, k + px, ds, k + pd, us, r + pu), (x, k, d, k, u, r)):
+        assert lib.hf_lowrank_down_ws(xx.data_ptr(), ldx, dd.data_ptr(), ldd, uu.data_ptr(), ldu, m, k, r,
+                                      ws.data_ptr(), nb, _stream(DEV)) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(us[:, :r], u)
+    assert bool((us[:, r:] == -1.0).all())
