@@ -26,6 +26,7 @@ parity-test shapes and supporting measurements, not the headline line):
      the fused q/k/v 5376->21504, out 7168->5376, gated up 5376->28672, down 14336->5376
   8  the standalone low-rank linear up(down(x)) (the model's non-INT8 linears) at M=37710, K->N 5376->7168 and
      14336->5376, ranks 64, 256 and 512: TFLOP/s of 2 M r (K + N), with the vendor library's bf16 GEMMs beside it
+     (the two alternate over three rounds; each reports its median round)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--config N [--rows M]]
 """
