@@ -59,7 +59,7 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-rows", type=int, default=32768, help="row sample for the CPU baseline")
     p.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5, 6, 7, 8),
-                   help="workload: 2 (default) is the headline QKV projection; 1, 3-7 are supporting measurements")
+                   help="workload: 2 (default) is the headline QKV projection; 1, 3-8 are supporting measurements")
     p.add_argument("--rows", type=int, default=None,
                    help="--config 5: only this M (64, 256 or 1024); --config 4: this many tokens (default 41344)")
     p.add_argument("--copy-probe", action="store_true",
