@@ -73,6 +73,23 @@ def test_gemm_i32_extreme_codes(oracle_lib):
     np.testing.assert_array_equal(acc.cpu().numpy(), oracle_lib.int8_gemm(a, b))
 
 
+@pytest.mark.parametrize("m,n,k", [(32768, 15360, 5120), (37710, 5376, 14336)])
+def test_gemm_i32_equals_the_vendor_int8_gemm_at_full_size(m, n, k):
+    """The int32 accumulator at the headline shape and the model's down projection against the vendor library's
+    INT8 GEMM (torch._int_mm, what the reference's cuBLASLt backend computes, int8.py:362): integer sums, so equal
+    everywhere."""
+    from hyperflow_h3_flash_amd.int8 import int8_gemm_i32
+
+    print(f"int32 accumulator against torch._int_mm M={m} N={n} K={k}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(m + n + k)
+    a = torch.randint(-127, 128, (m, k), device=DEV, dtype=torch.int8, generator=gen)
+    b = torch.randint(-127, 128, (n, k), device=DEV, dtype=torch.int8, generator=gen)
+    acc = int8_gemm_i32(a, b)
+    want = torch._int_mm(a, b.t())
+    torch.cuda.synchronize()
+    assert torch.equal(acc, want)
+
+
 # -------------------------------------------------------------------------------------------- rotate + quantize
 
 
