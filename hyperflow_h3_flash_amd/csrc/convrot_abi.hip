@@ -1111,7 +1111,7 @@ int hf_convrot_linear_ws(const uint16_t* x, int64_t ldx, int8_t* q, float* sx, i
     if (st != HF_OK) return st;
   } else if (!quantized && r > 0 && arithmetic == HF_ROTATE_BF16_DIV && lowrank_split_planned(M, K, r, ws, ws_bytes)) {
     // The low-rank projection splits K: it runs first and the rotation kernel adds its partial sums for the rows it
-    // rotates (one launch fewer; the same sums in the same order: config 1's layer 37.9 -> 35.1 us, M=1024, N=K=5120
+    // rotates (one launch fewer; the same sums in the same order: M=1024, K=N=3072, rank 32, bias 37.9 -> 35.1 us, M=1024, N=K=5120
     // 59.9 -> 57.4 us). Without a split the projection stays the last reader of x (its loads keep x out of the
     // Infinity Cache, over the codes the GEMM reads next): run first, it cost 0.6-0.8 % at M=32768 and M=256. The
     // rotation's arguments are checked before anything runs. The low-rank partials and the GEMM's partial planes

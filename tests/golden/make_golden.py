@@ -39,9 +39,9 @@ from oracle import oracle as O  # noqa: E402
 
 REFERENCE_INT8 = "/root/reference/src/hyperflow_h3_flash/int8.py"
 
-#: name, (M, K, N, G), generator options. Shapes follow the fixture plan for this path: a config-1-like slice,
+#: name, (M, K, N, G), generator options. Shapes follow the fixture plan for this path: a slice of the 1024-token K=N=3072 layer,
 #: the reference test's own (35, 128, 96, G=16), the kernel threshold M=17 at G=64, a single row, an odd M tail,
-#: a config-2-like slice, and one composition case with a rank-32 low-rank branch and a bias.
+#: a slice of the M=32768 QKV projection, and one composition case with a rank-32 low-rank branch and a bias.
 FIXTURES = [
     ("cfg1_slice", (64, 3072, 256, 256), dict(outlier_frac=0.01, outlier_scale=20.0, seed=11)),
     ("ref_test_shape", (35, 128, 96, 16), dict(outlier_frac=0.0, seed=12, weight_dist="quantized")),

@@ -1,7 +1,7 @@
 """Writes tests/golden/full/*.npz: the reference's own CPU path at two benchmark sizes, stored as digests.
 
 Runs in the development container only (the reference tree is not on the GPU machines). The small fixtures of
-``make_golden.py`` hold whole tensors; at the benchmark sizes (config 1: M=1024, K=N=3072; config 2: M=32768,
+``make_golden.py`` hold whole tensors; at the benchmark sizes (M=1024, K=N=3072; M=32768,
 K=5120, N=15360, the headline workload) the outputs are too large to commit, so each fixture stores:
 
 * the seed and generator options (the inputs are rebuilt by ``oracle.make_inputs`` anywhere, bit for bit);
@@ -12,7 +12,7 @@ K=5120, N=15360, the headline workload) the outputs are too large to commit, so 
 
 So a device output equal to the oracle everywhere becomes the reference's output once the listed positions are set
 to the reference's values, which the digests confirm over every element (``tests/test_gpu_full_reference.py``).
-Also config 3's FFN down projection (M=32768, K=13824, N=5120) and config 4's token count (M=41344) at the QKV width.
+Also the FFN down projection (M=32768, K=13824, N=5120) and a 41344-token block (M=41344) at the QKV width.
 
 The reference path is ``Int8RotLinear.forward`` on CPU tensors (``_forward_torch``, int8.py:173-179), loaded from
 ``src/hyperflow_h3_flash/int8.py`` by file path as in ``make_golden.py``. The oracle's rows are computed for every
@@ -39,12 +39,12 @@ sys.path.insert(0, HERE)
 from oracle import oracle as O  # noqa: E402
 from make_golden import Recorder, bits, from_bits, load_reference  # noqa: E402
 
-#: name, (M, K, N, G), generator options (config 1 and config 2 distributions; the Hadamard group is 256 because
+#: name, (M, K, N, G), generator options (the 1024-token layer's and the QKV projection's distributions; the Hadamard group is 256 because
 #: order 128 has no regular Hadamard matrix and the reference raises for it).
 FULL = [
     ("full_cfg1", (1024, 3072, 3072, 256), dict(outlier_frac=0.01, outlier_scale=20.0, seed=21)),
     ("full_cfg2", (32768, 5120, 15360, 256), dict(outlier_frac=0.005, outlier_scale=30.0, seed=22)),
-    # config 3's FFN down projection (deep K) and config 4's token count (40320 video + 1024 audio) at the QKV width
+    # the FFN down projection (deep K) and a 41344-token block (40320 video + 1024 audio) at the QKV width
     ("full_cfg3_down", (32768, 13824, 5120, 256), dict(outlier_frac=0.005, outlier_scale=30.0, seed=23)),
     ("full_cfg4_qkv", (41344, 5120, 15360, 256), dict(outlier_frac=0.005, outlier_scale=30.0, seed=24)),
 ]

@@ -1,8 +1,8 @@
 """The reference's own CPU path at four benchmark sizes against the oracle (CPU).
 
 The fixtures (tests/golden/full/*.npz) hold the reference ``Int8RotLinear.forward`` on CPU tensors at M=1024,
-K=N=3072 (config 1's layer), M=32768, K=5120, N=15360 (the headline QKV projection), M=32768, K=13824, N=5120
-(config 3's FFN down projection) and M=41344, K=5120, N=15360 (config 4's token count), as digests plus every
+K=N=3072 (a single layer of 1024 tokens), M=32768, K=5120, N=15360 (the headline QKV projection), M=32768, K=13824, N=5120
+(the FFN down projection) and M=41344, K=5120, N=15360 (a 41344-token block at the QKV width), as digests plus every
 position where it differs from the exact-sum definition. These tests check what the fixtures claim about those
 differences, and that the oracle reproduces the reference everywhere else on the rows it can afford to recompute:
 
@@ -10,7 +10,7 @@ differences, and that the oracle reproduces the reference everywhere else on the
   error bound of the exact sum on the reference's (`golden_utils.classify_rotation_mismatches`), and every listed
   code moves by one;
 * no scale differs, and every output that differs lies in a row whose codes differ;
-* config 1: the oracle's codes and scales of all 1024 rows give the reference's digest after the listed positions
+* M=1024, K=N=3072: the oracle's codes and scales of all 1024 rows give the reference's digest after the listed positions
   are set; the larger ones: the oracle's codes and outputs of the moved rows match the listed values, and its outputs
   of the sampled rows are the reference's.
 
@@ -60,7 +60,7 @@ def test_listed_differences_are_single_steps(name):
     assert fx["y_idx"].max(initial=-1) < m * n
 
 
-def test_config1_codes_and_scales_all_rows(oracle_lib):
+def test_m1024_codes_and_scales_all_rows(oracle_lib):
     fx = load("full_cfg1")
     inp = inputs(fx)
     g = int(fx["shape"][3])

@@ -1,8 +1,8 @@
 """The device path against the reference's own CPU path at four benchmark sizes, every element (GPU).
 
 tests/golden/full/*.npz hold the reference ``Int8RotLinear.forward`` on CPU tensors (int8.py:161-179) at M=1024,
-K=N=3072, at the headline shape M=32768, K=5120, N=15360, at config 3's FFN down projection M=32768, K=13824,
-N=5120 and at config 4's token count M=41344, K=5120, N=15360 (G=256, no low-rank branch, no bias) as SHA-256 digests
+K=N=3072, at the headline shape M=32768, K=5120, N=15360, at the FFN down projection M=32768, K=13824,
+N=5120 and at the 41344-token block's QKV width M=41344, K=5120, N=15360 (G=256, no low-rank branch, no bias) as SHA-256 digests
 of its codes and outputs, its scales in full, and the list of positions where it differs from the exact-sum
 definition (each explained by its fp32 accumulation; test_full_reference.py). Inputs are rebuilt from the seed.
 
