@@ -115,7 +115,7 @@ def test_split_planner_follows_the_measured_cost_models(lib):
 
 def test_workspace_queries_report_what_the_route_uses(lib):
     """The size queries follow the kernel route the call takes: no workspace for the one-pass few-row kernel
-    (M <= 64 with 32-row weight slices on a quarter to one round of CUs), for the 128-row band tiles (the M=1024, K=N=3072 layer's
+    (M <= 64 with 32-row weight slices on a quarter to one round of CUs), for the 128-row band tiles (the M=1024, K=N=3072
     layer) or for the 256 x 128 tiles, the split plan's partial planes otherwise; both tile kernels cover rank <= 64
     without SwiGLU, so the same sizes with rank 96 or SwiGLU take the split path and report its planes."""
     assert lib.hf_int8_linear_ws_bytes(64, 5120, 5120, 32, 0) == 0  # one pass

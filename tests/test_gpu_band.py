@@ -4,8 +4,8 @@ The shapes below are ones the host sends to that kernel on a 256-CU device: one 
 7/8 of the CUs while the 256 x 128 tiles would fill at most 3/4 (the test checks the rule on the device's CU count).
 Bars as for the other tile kernels: without a low-rank branch or bias the bf16 outputs are bitwise the oracle's (the
 reference's torch path); with them, within one bf16 ulp (2^-7 relative) of the fused definition and 1e-2 of the
-reference composition; the fused tanh-GELU against the oracle's GELU of the unfused output. Included: the M=1024, K=N=3072 layer's
-layer (M=1024, K=N=3072, rank 32, bias; 128 x 96 tiles), M=1024 with N=4096 and 5120 (128 x 128, 128 x 160), 768
+reference composition; the fused tanh-GELU against the oracle's GELU of the unfused output. Included: the single
+layer of 1024 tokens (M=1024, K=N=3072, rank 32, bias; 128 x 96 tiles), M=1024 with N=4096 and 5120 (128 x 128, 128 x 160), 768
 rows (128 x 128: six tile rows), ragged M and N with K not a multiple of the 128-byte stage, and K loops of two and
 three stages (the low-rank operands loaded with the first stages). The rows are computed independently, so the same
 rows through the persistent 256 x 256 tiles (as part of a 4096-row batch) agree bit for bit.
