@@ -150,3 +150,21 @@ def test_ceilings_library_loads_and_rejects_bad_arguments():
     assert lib.hf_ceiling_stream(buf, None, 64, 2, 1, 4, 1, buf, None) == -1
     assert lib.hf_ceiling_stream(buf, None, 64, 2, 0, 4, 1, None, None) == -1
     assert lib.hf_ceiling_stream(None, buf, 64, 1, 1, 4, 1, buf, None) == -1
+
+
+def test_one_call_layer_checks_the_rotation_before_the_low_rank_projection(lib):
+    """A layer whose low-rank projection splits K runs that projection before the rotation (the rotation kernel then
+    adds the partial sums of its rows); the rotation's arguments are still checked before anything is launched."""
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the calls below fail validation first
+    odd = ctypes.c_void_p((1 << 20) + 4)
+    m, n, k, r = 1024, 5120, 5120, 32
+    ws_bytes = lib.hf_convrot_linear_ws_bytes(m, n, k, r, 0)
+    assert ws_bytes > 0  # the projection splits K at this size
+
+    def call(x, group):
+        return lib.hf_convrot_linear_ws(x, k, fake, fake, 0, 0, fake, k, fake, fake, k, fake, r, r, None, 0, group,
+                                        fake, fake, n, m, n, k, fake, ws_bytes, None)
+
+    assert call(fake, 32) == -2  # 32 is not a power of 4
+    assert call(fake, 4096) == -2  # does not divide K
+    assert call(odd, 256) == -3  # x not 16-byte aligned
